@@ -1,0 +1,141 @@
+// C ABI entry points (include/ancha_hip.h): argument checks, the sticky failure state and
+// dispatch to the gfx950 kernels.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/ancha_hip.h"
+#include "kernels.hpp"
+
+namespace {
+
+std::atomic<int> g_sticky{0};
+thread_local std::string g_last;
+
+int fail(int code, const std::string& msg) {
+  g_last = msg;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* where) {
+  const int code = -static_cast<int>(e);
+  int expected = 0;
+  g_sticky.compare_exchange_strong(expected, code);
+  g_last = std::string(where) + ": " + hipGetErrorString(e);
+  return code;
+}
+
+int sticky() {
+  const int s = g_sticky.load();
+  if (s) g_last = "an earlier HIP call failed (sticky device failure " + std::to_string(s) + ")";
+  return s;
+}
+
+// Per-device cache: 1 = gfx950, 0 = other, -1 = unknown.
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_arch[kMaxDevices];
+std::atomic<bool> g_arch_init{false};
+
+bool device_is_gfx950() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return false;
+  if (!g_arch_init.exchange(true))
+    for (auto& a : g_arch) a.store(-1);
+  int known = g_arch[dev].load();
+  if (known < 0) {
+    hipDeviceProp_t prop;
+    known = hipGetDeviceProperties(&prop, dev) == hipSuccess &&
+                    std::strncmp(prop.gcnArchName, "gfx950", 6) == 0
+                ? 1
+                : 0;
+    g_arch[dev].store(known);
+  }
+  return known == 1;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+constexpr size_t kHeadDim = ANCHA_ATTENTION_HEAD_DIM;
+constexpr size_t kIntMax = 0x7fffffff;
+
+int run_attention(ancha::AttnParams& p, size_t groups, size_t tokens, size_t heads,
+                  hipStream_t stream, const char* name) {
+  if (groups == 0 || tokens == 0 || heads == 0) return ANCHA_HIP_OK;
+  if (!device_is_gfx950()) return fail(ANCHA_HIP_UNSUPPORTED, std::string(name) + ": not a gfx950 device");
+  const size_t qblocks = (tokens + 127) / 128;
+  if (tokens > kIntMax || groups * heads > kIntMax || groups * heads * qblocks > kIntMax)
+    return fail(ANCHA_HIP_UNSUPPORTED, std::string(name) + ": problem count exceeds the grid");
+  p.groups = static_cast<int>(groups);
+  p.tokens = static_cast<int>(tokens);
+  p.heads = static_cast<int>(heads);
+  const bool aligned = aligned16(p.q) && aligned16(p.k) && aligned16(p.v) && aligned16(p.out) &&
+                       (!p.rope || aligned16(p.rope)) && p.ldq % 4 == 0 && p.ldk % 4 == 0 &&
+                       p.ldv % 4 == 0;
+  const hipError_t e = ancha::launch_attention(p, aligned, stream);
+  if (e != hipSuccess) return hip_fail(e, name);
+  return ANCHA_HIP_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ancha_hip_available(void) {
+  int count = 0;
+  if (hipGetDeviceCount(&count) != hipSuccess || count <= 0) return 0;
+  return device_is_gfx950() ? 1 : 0;
+}
+
+int ancha_hip_attention(const float* q, const float* k, const float* v, size_t groups,
+                        size_t tokens, size_t heads, size_t ldq, size_t ldk, size_t ldv,
+                        const float* rope, float* out, hipStream_t stream) {
+  if (const int s = sticky()) return s;
+  const size_t span = heads * kHeadDim;
+  if (groups && tokens && heads && (!q || !k || !v || !out))
+    return fail(ANCHA_HIP_INVALID, "ancha_hip_attention: null tensor");
+  if (ldq < span || ldk < span || ldv < span)
+    return fail(ANCHA_HIP_INVALID,
+                "ancha_hip_attention: q / k / v column ranges do not fit the row stride");
+  ancha::AttnParams p{};
+  p.q = q;
+  p.k = k;
+  p.v = v;
+  p.gate = nullptr;
+  p.rope = rope;
+  p.out = out;
+  p.ldq = static_cast<long>(ldq);
+  p.ldk = static_cast<long>(ldk);
+  p.ldv = static_cast<long>(ldv);
+  p.ldg = 0;
+  return run_attention(p, groups, tokens, heads, stream, "ancha_hip_attention");
+}
+
+int ancha_hip_gated_attention(const float* packed, size_t groups, size_t tokens, size_t columns,
+                              size_t heads, const float* rope, float* out, hipStream_t stream) {
+  if (const int s = sticky()) return s;
+  if (columns < heads * (3 * kHeadDim + 1))
+    return fail(ANCHA_HIP_UNSUPPORTED,
+                "ancha_hip_gated_attention: columns < heads*(3*64+1)");
+  if (groups && tokens && heads && (!packed || !out))
+    return fail(ANCHA_HIP_INVALID, "ancha_hip_gated_attention: null tensor");
+  const size_t inner = heads * kHeadDim;
+  ancha::AttnParams p{};
+  p.q = packed;
+  p.k = packed + inner;
+  p.v = packed + 2 * inner;
+  p.gate = packed + 3 * inner;
+  p.rope = rope;
+  p.out = out;
+  p.ldq = p.ldk = p.ldv = p.ldg = static_cast<long>(columns);
+  return run_attention(p, groups, tokens, heads, stream, "ancha_hip_gated_attention");
+}
+
+int ancha_hip_check(void) { return g_sticky.load(); }
+
+const char* ancha_hip_last_error(void) { return g_last.c_str(); }
+
+}  // extern "C"

@@ -1,0 +1,190 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused RoFormer attention path on one MI355X.
+
+Default workload (the op the headline metric is quoted on): the time-axis fused attention
+over q, k, v float32 [G=120 (2 chunks x 60 bands), T=801 frames, H=8, d=64], N(0,1)/8 entries
+from seeds 1/2/3, RoPE (theta=10000) applied on load from the packed [4, 801, 64] table whose
+query half carries the 1/8 softmax scale. One step = one call of the op over the whole batch,
+inputs resident in HBM.
+
+Prints ONE JSON line: throughput in TFLOP/s (4*G*H*T^2*d per call), the live roofline of the
+attention kernel (HIP events over the timed region on the launch stream) and the restated
+reference CPU path (the oracle's materialized-tile attention) timed on the host's cores.
+
+`--workload band` measures the band-axis op [1602, 60, 8, 64] instead (HBM-bound roofline).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_MFMA_TFLOPS = 2500.0  # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0      # MI355X HBM3E
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cpu_threads() -> int:
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    limit = os.environ.get("OMP_NUM_THREADS")
+    if limit and limit.isdigit():
+        n = min(n, int(limit))
+    return max(1, n)
+
+
+def cpu_baseline(q, k, v, table, gpu_out, budget_s: float = 12.0) -> dict:
+    """The restated reference CPU path (oracle): RoPE tables applied on the host, then the
+    Flex-path materialized score tiles (roformer.rs:324-363) with groups split over all host
+    threads, on a bounded sample of the same groups. Median of 3 runs."""
+    import oracle as O
+
+    threads = cpu_threads()
+    G, T, H, D = q.shape
+    tq = table
+
+    def rotate(x, c, s):
+        sw = np.empty_like(x)
+        sw[..., 0::2], sw[..., 1::2] = x[..., 1::2], x[..., 0::2]
+        return (x * c[None, :, None, :] + sw * s[None, :, None, :]).astype(np.float32)
+
+    # Probe one group to size the sample.
+    g1 = max(1, min(G, threads))
+    sample = lambda n: [np.ascontiguousarray(a[:n]) for a in (q, k, v)]
+    qs, ks, vs = sample(g1)
+    t0 = time.perf_counter()
+    O.token_major_attention(rotate(qs, tq[0], tq[1]), rotate(ks, tq[2], tq[3]), vs,
+                            threads=threads)
+    probe = time.perf_counter() - t0
+    groups = int(min(G, max(g1, g1 * budget_s / 3.0 / max(probe, 1e-3))))
+    groups = max(threads, groups // threads * threads) if groups >= threads else groups
+    groups = min(groups, G)
+    qs, ks, vs = sample(groups)
+    times, out = [], None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        qr, kr = rotate(qs, tq[0], tq[1]), rotate(ks, tq[2], tq[3])
+        out = O.token_major_attention(qr, kr, vs, threads=threads)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    flops = 4.0 * groups * H * T * T * D
+    err = float(np.abs(out - gpu_out[:groups]).max())
+    return {
+        "value": round(flops / t / 1e12, 5),
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"{groups} of {G} groups x {H} heads, T={T}: host RoPE + materialized "
+                   f"fp32 score tiles, groups over {threads} threads, median of 3 "
+                   f"({t:.2f} s)"),
+        "max_abs_vs_gpu": err,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", choices=["time", "band"], default="time")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path "
+              "(chunk-level data parallelism would need no communication). Run with --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+
+    from ancha_amd import fused
+    from ancha_amd import workload as W
+
+    if not torch.cuda.is_available() or not fused.available():
+        print("bench.py needs an MI355X (gfx950) GPU and the built kernel library",
+              file=sys.stderr)
+        return 2
+    dev = torch.device("cuda:0")
+    shape = W.TIME_SHAPE if args.workload == "time" else W.BAND_SHAPE
+    G, T, H, D = shape
+    log(f"generating q, k, v {shape} on the GPU")
+    q, k, v = (W.normal_torch(shape, s, 1.0 / 8.0, device=dev) for s in (1, 2, 3))
+    table_np = W.axis_rope_packed(W.rope_freqs(), T)
+    table = torch.from_numpy(table_np).to(dev)
+    torch.cuda.synchronize()
+
+    def step():
+        return fused.attention(q, k, v, rope=table)
+
+    out = step()
+    assert out is not None, "attention kernel rejected the workload"
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        out = step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = start.elapsed_time(end) / args.steps
+    flops = 4.0 * G * H * T * T * D
+    io_bytes = 4.0 * 4 * G * T * H * D  # q, k, v read + out written, fp32
+    value = flops * args.steps / wall / 1e12
+    log(f"{args.workload}: {kernel_ms * 1e3:.1f} us/launch, {flops / kernel_ms / 1e9:.1f} TFLOP/s, "
+        f"{io_bytes / kernel_ms / 1e6:.0f} GB/s")
+    if args.workload == "time":
+        achieved = flops / (kernel_ms * 1e-3) / 1e12
+        roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
+                    "traffic": None}
+    else:
+        achieved = io_bytes / (kernel_ms * 1e-3) / 1e9
+        roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+    result = {
+        "metric": "fused attn TFLOP/s (% MFMA peak)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: seeded N(0,1)/8 q, k, v (splitmix64 + Box-Muller)",
+        "config": {"workload": f"{args.workload}-axis fused attention, RoPE on load",
+                   "groups": G, "tokens": T, "heads": H, "head_dim": D,
+                   "io": "fp32", "mfma_operands": "fp16", "accumulate": "fp32",
+                   "parallelism": "single GPU"},
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("timing the restated reference CPU path")
+        result["cpu_baseline"] = cpu_baseline(q.cpu().numpy(), k.cpu().numpy(),
+                                              v.cpu().numpy(), table_np, out.cpu().numpy())
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,177 @@
+"""Parity of the gfx950 attention kernels (through the C ABI) with the oracle.
+
+Tolerance: max-abs <= 2e-3 on the attention block, the bound the fused path is held to
+(fp16 MFMA operands with fp32 accumulation and an fp32 softmax vs the reference's fp32 CPU
+path). Cases mirror tests/cuda_contracts.rs:196-251 of the reference plus the two production
+shapes (time axis T=801, band axis S=60) and their edges.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from ancha_amd import fused
+from ancha_amd import workload as W
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-3
+
+
+def wave(shape, shift):
+    n = int(np.prod(shape))
+    i = np.arange(n, dtype=np.float32)
+    return np.tanh(np.sin(i * np.float32(0.731) + np.float32(shift)) * np.float32(1.7)).astype(
+        np.float32).reshape(shape)
+
+
+def dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(gpu)
+
+
+def report(name, err):
+    print(f"{name}: max|diff| {err:.3e}", flush=True)
+
+
+@pytest.mark.parametrize("groups,tokens,heads,strided",
+                         [(2, 1, 1, False), (3, 63, 2, False), (2, 65, 1, True),
+                          (1, 130, 3, False)])
+def test_fused_attention_matches_reference_cases(gpu, groups, tokens, heads, strided):
+    width = 128 if strided else 64
+    raw = [wave((groups, tokens, heads, width), s)[..., :64] for s in (0.1, 1.3, 2.9)]
+    q, k, v = raw[0] * np.float32(0.4), raw[1], raw[2]
+    qs = q * np.float32(0.125)
+    expected = O.attention_op(qs, k, v)
+    if strided:
+        full = [dev(wave((groups, tokens, heads, width), s), gpu) for s in (0.1, 1.3, 2.9)]
+        tq = full[0][..., :64] * 0.4 * 0.125
+        tk, tv = full[1][..., :64], full[2][..., :64]
+    else:
+        tq, tk, tv = dev(qs, gpu), dev(k, gpu), dev(v, gpu)
+    got = fused.attention(tq, tk, tv)
+    assert got is not None and tuple(got.shape) == (groups, tokens, heads, 64)
+    err = np.abs(got.cpu().numpy() - expected).max()
+    report(f"attention {groups}x{tokens}x{heads}", err)
+    assert err < TOL
+
+    # The packed RoFormer layout: q | k | v | per-head gates | 5 zero columns (unaligned rows).
+    gates = wave((groups, tokens, heads), 4.4) * np.float32(3.0)
+    flat = lambda a: a.reshape(groups, tokens, heads * 64)
+    packed = np.concatenate([flat(qs), flat(k), flat(v), gates,
+                             np.zeros((groups, tokens, 5), np.float32)], axis=2)
+    got = fused.gated_attention(dev(packed, gpu), heads)
+    gated = expected / (1.0 + np.exp(-gates.astype(np.float64)))[..., None]
+    err = np.abs(got.cpu().numpy() - gated).max()
+    report(f"gated {groups}x{tokens}x{heads}", err)
+    assert err < TOL
+
+
+def test_unsupported_shapes_return_none(gpu):
+    narrow = dev(wave((1, 8, 1, 32), 0.0), gpu)
+    assert fused.attention(narrow, narrow, narrow) is None
+    packed = dev(np.zeros((1, 8, 3 * 64), np.float32), gpu)
+    assert fused.gated_attention(packed, 1) is None
+
+
+def seeded(shape, gpu):
+    q, k, v = (W.normal_torch(shape, s, 1.0 / 8.0, device=gpu) for s in (1, 2, 3))
+    return q, k, v
+
+
+def oracle_slice(q, k, v, table, groups):
+    """Oracle (fp64) output for the listed groups."""
+    idx = torch.tensor(groups, device=q.device)
+    pick = lambda t: t.index_select(0, idx).cpu().numpy()
+    return O.attention_op(pick(q), pick(k), pick(v), rope=table)
+
+
+@pytest.mark.parametrize("tokens", [2, 60, 62, 64, 65, 127, 128, 129, 801, 1101])
+def test_rope_on_load_matches_oracle(gpu, tokens):
+    groups = 3 if tokens > 200 else 5
+    q, k, v = seeded((groups, tokens, 8, 64), gpu)
+    table = W.axis_rope_packed(W.rope_freqs(), tokens)
+    got = fused.attention(q, k, v, rope=dev(table, gpu)).cpu().numpy()
+    expected = O.attention_op(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), rope=table)
+    err = np.abs(got - expected).max()
+    report(f"rope T={tokens}", err)
+    assert err < TOL
+
+
+def test_rope_on_load_equals_prerotated_inputs(gpu):
+    # The two boundary modes agree: rotation in the kernel vs q/k rotated (and q scaled) by
+    # the caller, as the reference's GEMM epilogue does.
+    tokens = 801
+    q, k, v = seeded((2, tokens, 8, 64), gpu)
+    table = W.axis_rope_packed(W.rope_freqs(), tokens)
+    tq = dev(table, gpu)
+
+    def rotate(x, c, s):
+        sw = torch.stack([x[..., 1::2], x[..., 0::2]], dim=-1).reshape(x.shape)
+        return x * c[None, :, None, :] + sw * s[None, :, None, :]
+
+    qr, kr = rotate(q, tq[0], tq[1]), rotate(k, tq[2], tq[3])
+    a = fused.attention(q, k, v, rope=tq)
+    b = fused.attention(qr, kr, v)
+    err = (a - b).abs().max().item()
+    report("rope modes", err)
+    assert err < TOL
+
+
+def test_time_axis_full_size(gpu):
+    """The time-axis op at its production size [120, 801, 8, 64], RoPE on load: sampled groups
+    against the oracle, every output checked finite and inside the convex hull of v."""
+    q, k, v = seeded(W.TIME_SHAPE, gpu)
+    table = W.axis_rope_packed(W.rope_freqs(), W.TIME_SHAPE[1])
+    out = fused.attention(q, k, v, rope=dev(table, gpu))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    lo, hi = v.amin(dim=1, keepdim=True), v.amax(dim=1, keepdim=True)
+    assert (out >= lo - TOL).all() and (out <= hi + TOL).all()
+    groups = [0, 61, 119]
+    expected = oracle_slice(q, k, v, table, groups)
+    err = np.abs(out[groups].cpu().numpy() - expected).max()
+    report("time full-size", err)
+    assert err < TOL
+    again = fused.attention(q, k, v, rope=dev(table, gpu))
+    assert torch.equal(out, again), "kernel must be deterministic"
+
+
+def test_band_axis_full_size(gpu):
+    """The band-axis op at its production size [1602, 60, 8, 64]."""
+    q, k, v = seeded(W.BAND_SHAPE, gpu)
+    table = W.axis_rope_packed(W.rope_freqs(), W.BAND_SHAPE[1])
+    out = fused.attention(q, k, v, rope=dev(table, gpu))
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    groups = [0, 1, 800, 1601]
+    expected = oracle_slice(q, k, v, table, groups)
+    err = np.abs(out[groups].cpu().numpy() - expected).max()
+    report("band full-size", err)
+    assert err < TOL
+
+
+@pytest.mark.parametrize("tokens", [60, 801])
+def test_gated_attention_production_layout(gpu, tokens):
+    """The Mel-RoFormer packed projection: [G, T, 1664] = q | k | v (512 each) | 8 gates | pad,
+    RoPE on load."""
+    groups, heads = 4, 8
+    packed = W.normal_torch((groups, tokens, 1664), 9, 0.5, device=gpu)
+    table = W.axis_rope_packed(W.rope_freqs(), tokens)
+    got = fused.gated_attention(packed, heads, rope=dev(table, gpu)).cpu().numpy()
+    expected = O.gated_attention(packed.cpu().numpy(), heads, rope=table)
+    err = np.abs(got - expected).max()
+    report(f"gated production T={tokens}", err)
+    assert err < TOL
+
+
+def test_runs_on_a_side_stream(gpu):
+    q, k, v = seeded((2, 801, 8, 64), gpu)
+    ref = fused.attention(q, k, v)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        got = fused.attention(q, k, v)
+    torch.cuda.current_stream().wait_stream(s)
+    assert torch.equal(ref, got)
