@@ -5,71 +5,116 @@
 //
 // Both kernels compute S^T = K.Q^T and O^T = V^T.P^T with v_mfma_f32_16x16x32_f16, so that the
 // score tile produced by the first product is already, lane for lane, the B operand of the
-// second: each lane owns one query column and 4+4 keys of every 32-key step. The online softmax
-// runs in fp32 in the log2 domain (q carries log2(e)), the row max/sum reductions are two
-// cross-lane shuffles, and the 1/l normalisation and the gate are applied once at the end.
+// second: each lane owns one query column and 4+4 keys of every 32-key step. The softmax runs
+// in fp32 in the log2 domain (q carries log2(e)); row maxima are two cross-lane shuffles, row
+// sums come from the MFMA (a ones matrix times P^T, so numerator and denominator see the same
+// fp16-rounded probabilities), and 1/l and the gate are applied once in the epilogue.
 //
-//  * attention_time_kernel: long sequences (the time axis, T ~ 801). One workgroup = 4 waves =
-//    128 queries of one (group, head); 64-key K / V^T tiles are staged in LDS as fp16, double
-//    buffered, the next tile's global loads in flight while the current one is multiplied.
+// All global traffic goes through raw buffer loads/stores whose hardware range check returns 0
+// for rows at or past `tokens` (and drops stores there), so ragged tails need no branches.
+//
+//  * attention_time_kernel: long sequences (the time axis, T ~ 801). One workgroup = 8 waves x
+//    64 queries of one (group, head); 64-key K / V^T tiles are staged in LDS as fp16 (K rotated
+//    on the way), double buffered, the next tile's loads in flight while the current one is
+//    multiplied. The online softmax rescales lazily: the running maximum only moves when a
+//    tile exceeds it by more than kTau, so most tiles skip the O / l rescale.
 //  * attention_band_kernel: T <= 64 (the band axis, 60-62 bands, huge batch). One wave owns one
 //    whole (group, head) problem: K and Q fragments come straight from global memory into
 //    registers, V goes through a wave-private LDS transpose, softmax is exact (one key tile).
+#include <type_traits>
+
 #include "common.hpp"
 #include "kernels.hpp"
 
 namespace ancha {
 
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+
+// Raw buffer over [base, base + bytes): loads past the end return 0, stores there are dropped.
+// Callers pass wave-uniform values; readfirstlane states that, so the descriptor lives in SGPRs
+// (a descriptor the compiler believes divergent costs a readfirstlane loop per access).
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, unsigned bytes) {
+  const unsigned long long a = reinterpret_cast<unsigned long long>(base);
+  const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)a);
+  const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(a >> 32));
+  void* uniform = reinterpret_cast<void*>(((unsigned long long)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(uniform, 0, __builtin_amdgcn_readfirstlane(bytes),
+                                           0x00020000);
+}
+
 template <bool ALIGNED>
-__device__ __forceinline__ float4 load4(const float* p) {
+__device__ __forceinline__ float4 bload4(rsrc_t r, unsigned off) {
   if constexpr (ALIGNED) {
-    return *reinterpret_cast<const float4*>(p);
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   } else {
-    return make_float4(p[0], p[1], p[2], p[3]);
+    return make_float4(__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 8, 0, 0)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 12, 0, 0)));
   }
 }
 
 template <bool ALIGNED>
-__device__ __forceinline__ void store4(float* p, float4 v) {
+__device__ __forceinline__ void bstore4(rsrc_t r, unsigned off, float4 v) {
   if constexpr (ALIGNED) {
-    *reinterpret_cast<float4*>(p) = v;
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
   } else {
-    p[0] = v.x;
-    p[1] = v.y;
-    p[2] = v.z;
-    p[3] = v.w;
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.x), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.y), r, off + 4, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.z), r, off + 8, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.w), r, off + 12, 0, 0);
   }
+}
+
+__device__ __forceinline__ float bload1(rsrc_t r, unsigned off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
 }
 
 __device__ __forceinline__ float comp(float4 v, int j) {
   return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
 }
 
+// Interleaved rotation of channels (2i, 2i+1), (2i+2, 2i+3) by pair angles with cosines
+// (c0, c1) and sines (s0, s1): the same x*cos + swap_pairs(x)*sin as the packed table encodes
+// ([c, c] cosine pairs, [-s, s] sine pairs), from only the distinct table values.
+__device__ __forceinline__ float4 rotate_pairs(float4 x, float c0, float c1, float s0, float s1) {
+  return make_float4(x.x * c0 - x.y * s0, x.y * c0 + x.x * s0, x.z * c1 - x.w * s1,
+                     x.w * c1 + x.z * s1);
+}
+
+// Lazy-rescale threshold in log2 units: unnormalised probabilities stay below 2^kTau (fp16-safe).
+constexpr float kTau = 8.0f;
+// s_waitcnt operand (GFX9 encoding) waiting for all vector memory operations: vmcnt(0),
+// expcnt and lgkmcnt left at their maxima.
+constexpr int kWaitVmem = 0x0F70;
+// fp16 1.0 in both halves of a dword: the A operand of the row-sum MFMA.
+constexpr unsigned kOnesH2 = 0x3C003C00u;
+
 // 8-byte chunk swizzle of a transposed V^T row `d` (64 keys = 16 chunks of 4 fp16): keeps both
 // the 4x4-block transposing writes and the MFMA operand reads free of LDS bank conflicts.
 __device__ __forceinline__ int vt_swizzle(int d) { return ((d >> 2) ^ (d << 2)) & 15; }
 
-// Loads 8 consecutive channels [d, d+8) of row t (zero when t >= T), applies the rotary table
-// rows (cos at table `ct`, signed sin at `ct + 1`) when ROPE, scales, and packs to fp16.
+// Byte offset of 16-byte chunk c (8 fp16 channels) of K row r in a [64][64] fp16 tile.
+__device__ __forceinline__ int k_offset(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+
+// Channels [d, d+8) of row t (0 past the end), rotated with the table rows (cos at table ct,
+// signed sin at ct + 1) when ROPE, scaled, packed to fp16.
 template <bool ROPE, bool ALIGNED>
-__device__ __forceinline__ u32x4 load_fragment(const float* base, long ld, int t, int T, int d,
-                                               const float* rope, int ct, float scale) {
-  float4 a = make_float4(0.f, 0.f, 0.f, 0.f), b = a;
-  if (t < T) {
-    const float* src = base + (long)t * ld + d;
-    a = load4<ALIGNED>(src);
-    b = load4<ALIGNED>(src + 4);
-    if constexpr (ROPE) {
-      const float* c = rope + ((long)ct * T + t) * 64 + d;
-      const float* s = c + (long)T * 64;
-      a = rotate4(a, load4<ALIGNED>(c), load4<ALIGNED>(s));
-      b = rotate4(b, load4<ALIGNED>(c + 4), load4<ALIGNED>(s + 4));
-    }
-    a = scale4(a, scale);
-    b = scale4(b, scale);
+__device__ __forceinline__ u32x4 load_fragment(rsrc_t x, unsigned ld4, rsrc_t table, int T, int t,
+                                               int d, int ct, float scale) {
+  const unsigned off = (unsigned)t * ld4 + d * 4;
+  float4 a = bload4<ALIGNED>(x, off), b = bload4<ALIGNED>(x, off + 16);
+  if constexpr (ROPE) {
+    // cos values at even channels of table ct, +sin values at odd channels of table ct + 1.
+    const unsigned c = ((unsigned)(ct * T + t) * 64 + d) * 4, s = c + (unsigned)T * 256 + 4;
+    a = rotate_pairs(a, bload1(table, c), bload1(table, c + 8), bload1(table, s),
+                     bload1(table, s + 8));
+    b = rotate_pairs(b, bload1(table, c + 16), bload1(table, c + 24), bload1(table, s + 16),
+                     bload1(table, s + 24));
   }
-  return u32x4{pack_h2(a.x, a.y), pack_h2(a.z, a.w), pack_h2(b.x, b.y),
-               pack_h2(b.z, b.w)};
+  a = scale4(a, scale);
+  b = scale4(b, scale);
+  return u32x4{pack_h2(a.x, a.y), pack_h2(a.z, a.w), pack_h2(b.x, b.y), pack_h2(b.z, b.w)};
 }
 
 // Writes a 4-key x 4-channel block (rows r = 0..3 of `vr` are keys 4*kq+r, channels 4*dq..+3)
@@ -96,184 +141,359 @@ __device__ __forceinline__ u32x4 vt_fragment(const unsigned char* vt, int db, in
   return u32x4{lo.x, lo.y, hi.x, hi.y};
 }
 
+// Chunked V^T tile (time kernel): row d holds the 64 keys of channel d, and the 16-byte chunk
+// ks*4 + grp holds keys ks*32 + {grp*4 + i, 16 + grp*4 + i} (i = 0..3) in that order, so one
+// chunk is exactly one lane's A operand of O^T = V^T.P^T. Chunks are XOR-swizzled by d & 7.
+__device__ __forceinline__ int vtc_offset(int d, int key) {
+  const int chunk = (key >> 5) * 4 + ((key & 15) >> 2);
+  const int elem = (key & 3) + ((key & 16) >> 2);
+  return d * 128 + ((chunk ^ (d & 7)) << 4) + elem * 2;
+}
+
 // B operand of O^T = V^T.P^T from the score tiles of key blocks 2ks and 2ks+1.
 __device__ __forceinline__ u32x4 p_fragment(f32x4 a, f32x4 b) {
   return u32x4{pack_h2(a[0], a[1]), pack_h2(a[2], a[3]), pack_h2(b[0], b[1]),
                pack_h2(b[2], b[3])};
 }
 
-// Final 1/l and sigmoid(gate) scaling and store of one lane's 16 channels of query t.
+// Output rows of one (group, head): [tokens, heads*64] starting at channel 64*h.
+struct OutRows {
+  rsrc_t out, gate;
+  unsigned ld4, ldg4;
+};
+
+__device__ __forceinline__ OutRows out_rows(const AttnParams& p, int g, int h) {
+  const int T = p.tokens;
+  OutRows o;
+  o.ld4 = (unsigned)p.heads * 256;
+  o.out = make_rsrc(p.out + ((long)g * T * p.heads + h) * 64, (unsigned)(T - 1) * o.ld4 + 256);
+  o.ldg4 = (unsigned)p.ldg * 4;
+  o.gate = make_rsrc(p.gate ? p.gate + (long)g * T * p.ldg + h : p.out,
+                     p.gate ? (unsigned)(T - 1) * o.ldg4 + 4 : 0);
+  return o;
+}
+
+// 1/l and sigmoid(gate) scaling and store of one lane's 16 channels (grp*4 + 16*db) of query t.
 template <bool GATED, bool ALIGNED>
-__device__ __forceinline__ void store_output(const AttnParams& p, const f32x4 (&o)[4], float l,
-                                             int g, int h, int t, int grp) {
+__device__ __forceinline__ void store_output(const OutRows& o, const f32x4 (&acc)[4], float l,
+                                             int t, int grp) {
   float scale = 1.0f / l;
-  if constexpr (GATED) {
-    const float gate = p.gate[((long)g * p.tokens + t) * p.ldg + h];
-    scale = scale / (1.0f + expf(-gate));
-  }
-  float* dst = p.out + (((long)g * p.tokens + t) * p.heads + h) * 64 + grp * 4;
+  if constexpr (GATED) scale = scale / (1.0f + expf(-bload1(o.gate, (unsigned)t * o.ldg4)));
+  const unsigned base = (unsigned)t * o.ld4 + grp * 16;
 #pragma unroll
   for (int db = 0; db < 4; db++)
-    store4<ALIGNED>(dst + db * 16, make_float4(o[db][0] * scale, o[db][1] * scale,
-                                               o[db][2] * scale, o[db][3] * scale));
+    bstore4<ALIGNED>(o.out, base + db * 64,
+                     make_float4(acc[db][0] * scale, acc[db][1] * scale, acc[db][2] * scale,
+                                 acc[db][3] * scale));
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Maximum over the four lanes {l, l^16, l^32, l^48} holding one column of an MFMA tile, with
+// the gfx950 row-swap permutes (each returns the lane's own value and its partner's).
+// (The swap results are copied to scalars before reinterpreting: bit-casting a vector element
+// lvalue directly would read element 0.)
+__device__ __forceinline__ float column_max(float x) {
+  const unsigned xb = __builtin_bit_cast(unsigned, x);
+  const auto a = __builtin_amdgcn_permlane32_swap(xb, xb, false, false);
+  const unsigned a0 = a[0], a1 = a[1];
+  const float y = fmaxf(__builtin_bit_cast(float, a0), __builtin_bit_cast(float, a1));
+  const unsigned yb = __builtin_bit_cast(unsigned, y);
+  const auto b = __builtin_amdgcn_permlane16_swap(yb, yb, false, false);
+  const unsigned b0 = b[0], b1 = b[1];
+  return fmaxf(__builtin_bit_cast(float, b0), __builtin_bit_cast(float, b1));
+}
+
+// acc *= s, written so the result stays in acc's registers: a conditional rescale then costs
+// nothing on the path that skips it (no register copies where the two paths join).
+__device__ __forceinline__ void scale_in_place(f32x4& acc, float s) {
+#pragma unroll
+  for (int i = 0; i < 4; i++) asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[i]) : "v"(s));
 }
 
 // ------------------------------------------------------------------------------------------
-// Long sequences: 4 waves x 32 queries of one (group, head) per workgroup.
+// Long sequences: 8 waves x 64 queries of one (group, head) per workgroup (one per CU).
 // ------------------------------------------------------------------------------------------
+constexpr int kTimeWaves = 8;
+constexpr int kTimeQueries = kTimeWaves * 64;
+
 template <bool GATED, bool ROPE, bool ALIGNED>
-__global__ __launch_bounds__(256) void attention_time_kernel(AttnParams p, int qblocks,
-                                                             int total) {
+__global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnParams p, int qblocks,
+                                                                         int total) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_k[2][64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_v[2][64 * 128];
+  // Each wave's 64 rotated, log2(e)-scaled fp16 queries, laid out like a K tile.
+  __shared__ __attribute__((aligned(16))) unsigned char lds_q[kTimeWaves][64 * 128];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int col = lane & 15, grp = lane >> 4;
   const int logical = xcd_remap(blockIdx.x, total);
   const int qblk = logical % qblocks, gh = logical / qblocks;
   const int h = gh % p.heads, g = gh / p.heads;
   const int T = p.tokens;
-  const float* qg = p.q + (long)g * T * p.ldq + h * 64;
-  const float* kg = p.k + (long)g * T * p.ldk + h * 64;
-  const float* vg = p.v + (long)g * T * p.ldv + h * 64;
-  const int q0 = qblk * 128 + wave * 32;
+  const unsigned ldq4 = (unsigned)p.ldq * 4, ldk4 = (unsigned)p.ldk * 4,
+                 ldv4 = (unsigned)p.ldv * 4;
+  const float* kbase = p.k + (long)g * T * p.ldk + h * 64;
+  const float* vbase = p.v + (long)g * T * p.ldv + h * 64;
+  const int q0 = qblk * kTimeQueries + wave * 64;
   const bool active = q0 < T;
 
-  // B operand of S^T = K.Q^T: query qb*16 + col, channels ds*32 + grp*8 .. +7, log2(e) folded.
-  u32x4 qf[2][2];
-#pragma unroll
-  for (int qb = 0; qb < 2; qb++)
-#pragma unroll
-    for (int ds = 0; ds < 2; ds++)
-      qf[qb][ds] = load_fragment<ROPE, ALIGNED>(qg, p.ldq, q0 + qb * 16 + col, T,
-                                                ds * 32 + grp * 8, p.rope, 0, kLog2e);
+  // B operand of S^T = K.Q^T (query q0 + qb*16 + col, channels ds*32 + grp*8 .. +7) is read
+  // per work unit from this wave's LDS rows, staged once below.
+  unsigned char* Q = lds_q[wave];
 
-  // Tile staging: thread owns key rows (tid>>4) + 16*it of K at channels 4*(tid&15), and the
-  // 4x4 V block (keys 4*(tid>>4)..+3, channels 4*(tid&15)..+3).
+  // Tile staging (512 threads): thread owns K rows lrow and lrow + 32 at channels 4*lchunk,
+  // and the 2-key x 4-channel V block (keys 2*lrow, 2*lrow + 1). Offsets are relative to
+  // per-tile buffer descriptors, so they stay fixed across tiles.
   const int lrow = tid >> 4, lchunk = tid & 15;
-  float4 kreg[4], kcos[4], ksin[4], vreg[4];
+  const unsigned koff = (unsigned)lrow * ldk4 + lchunk * 16;
+  const unsigned voff = (unsigned)(2 * lrow) * ldv4 + lchunk * 16;
+  const unsigned toff = (unsigned)lrow * 256 + lchunk * 16;
+  float4 kreg[2], vreg[2];
+  float2 kcos[2], ksin[2];
   auto load_tile = [&](int key0) {
+    const unsigned rows = (unsigned)(T - key0);
+    const rsrc_t kr = make_rsrc(kbase + (long)key0 * p.ldk, (rows - 1) * ldk4 + 256);
+    const rsrc_t vr = make_rsrc(vbase + (long)key0 * p.ldv, (rows - 1) * ldv4 + 256);
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const int t = key0 + lrow + 16 * it;
-      const bool ok = t < T;
-      kreg[it] = ok ? load4<ALIGNED>(kg + (long)t * p.ldk + lchunk * 4)
-                    : make_float4(0.f, 0.f, 0.f, 0.f);
-      if constexpr (ROPE) {
-        const float* c = p.rope + ((long)2 * T + (ok ? t : 0)) * 64 + lchunk * 4;
-        kcos[it] = load4<ALIGNED>(c);
-        ksin[it] = load4<ALIGNED>(c + (long)T * 64);
+    for (int it = 0; it < 2; it++) kreg[it] = bload4<ALIGNED>(kr, koff + it * 32 * ldk4);
+#pragma unroll
+    for (int r = 0; r < 2; r++) vreg[r] = bload4<ALIGNED>(vr, voff + r * ldv4);
+    if constexpr (ROPE) {
+      // Key cos rows (table 2) and +sin values (odd channels of table 3) of this tile.
+      const rsrc_t cr = make_rsrc(p.rope + (long)(2 * T + key0) * 64, rows * 256);
+      const rsrc_t sr = make_rsrc(p.rope + (long)(3 * T + key0) * 64, rows * 256);
+#pragma unroll
+      for (int it = 0; it < 2; it++) {
+        const unsigned o = toff + it * 32 * 256;
+        kcos[it] = make_float2(bload1(cr, o), bload1(cr, o + 8));
+        ksin[it] = make_float2(bload1(sr, o + 4), bload1(sr, o + 12));
       }
-    }
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-      const int t = key0 + lrow * 4 + r;
-      vreg[r] = t < T ? load4<ALIGNED>(vg + (long)t * p.ldv + lchunk * 4)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
     }
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const int r = lrow + 16 * it;
+    for (int it = 0; it < 2; it++) {
+      const int r = lrow + 32 * it;
       float4 x = kreg[it];
-      if constexpr (ROPE) x = rotate4(x, kcos[it], ksin[it]);
+      if constexpr (ROPE) x = rotate_pairs(x, kcos[it].x, kcos[it].y, ksin[it].x, ksin[it].y);
       const u32x2 w = {pack_h2(x.x, x.y), pack_h2(x.z, x.w)};
-      *reinterpret_cast<u32x2*>(lds_k[buf] + r * 128 + ((((lchunk >> 1) ^ (r & 7))) << 4) +
-                                ((lchunk & 1) << 3)) = w;
+      *reinterpret_cast<u32x2*>(lds_k[buf] + k_offset(r, lchunk >> 1) + ((lchunk & 1) << 3)) = w;
     }
-    store_vt_block(lds_v[buf], vreg, lrow, lchunk);
+    // V^T rows 4*lchunk + j get the key pair (2*lrow, 2*lrow + 1) as one dword.
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const unsigned w = pack_h2(comp(vreg[0], j), comp(vreg[1], j));
+      *reinterpret_cast<unsigned*>(lds_v[buf] + vtc_offset(lchunk * 4 + j, 2 * lrow)) = w;
+    }
   };
 
-  f32x4 o[4][2];
+  f32x4 o[4][4];
+  float lsum[4];
+  // Running maximum per query block (log2 units). Scores come out of the MFMA as s - m
+  // because the S accumulators are seeded with -m.
+  float m[4];
 #pragma unroll
-  for (int db = 0; db < 4; db++)
+  for (int qb = 0; qb < 4; qb++) {
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) o[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[2] = {kMasked, kMasked}, l[2] = {0.f, 0.f};
+    for (int db = 0; db < 4; db++) o[db][qb] = zero4();
+    lsum[qb] = 0.f;
+  }
 
   const int ntiles = (T + 63) / 64;
   load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int j = 0; j < ntiles; j++) {
-    const int buf = j & 1;
-    if (j + 1 < ntiles) load_tile((j + 1) * 64);
-    if (active) {
-      const unsigned char* K = lds_k[buf];
-      const unsigned char* V = lds_v[buf];
-      // S^T[key kb*16 + grp*4 + r][query qb*16 + col] in s[kb][qb][r].
-      f32x4 s[4][2];
+  if (active) {
+    // Stage this wave's 64 query rows: coalesced row loads (16 lanes per 256-byte row), RoPE
+    // with the query table rows (carrying 1/sqrt(64)), log2(e), fp16, into the K-tile layout.
+    const unsigned rows = (unsigned)(T - q0);
+    const rsrc_t qr = make_rsrc(p.q + ((long)g * T + q0) * p.ldq + h * 64, (rows - 1) * ldq4 + 256);
+    const rsrc_t cr = make_rsrc(ROPE ? p.rope + (long)q0 * 64 : p.q, ROPE ? rows * 256 : 0);
+    const rsrc_t sr = make_rsrc(ROPE ? p.rope + (long)(T + q0) * 64 : p.q, ROPE ? rows * 256 : 0);
+    const int chunk = lane & 15;
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++) {
-        s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-        s[kb][1] = s[kb][0];
-        const int r = kb * 16 + col;
-#pragma unroll
-        for (int ds = 0; ds < 2; ds++) {
-          const int c16 = ds * 4 + grp;
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(K + r * 128 + ((c16 ^ (r & 7)) << 4));
-          s[kb][0] = mfma16x16x32(kf, qf[0][ds], s[kb][0]);
-          s[kb][1] = mfma16x16x32(kf, qf[1][ds], s[kb][1]);
-        }
+    for (int it = 0; it < 16; it++) {
+      const int r = it * 4 + (lane >> 4);
+      float4 x = bload4<ALIGNED>(qr, (unsigned)r * ldq4 + chunk * 16);
+      if constexpr (ROPE) {
+        const unsigned t = (unsigned)r * 256 + chunk * 16;
+        x = rotate4(x, bload4<ALIGNED>(cr, t), bload4<ALIGNED>(sr, t));
       }
-      const int key0 = j * 64;
-      if (key0 + 64 > T) {
+      x = scale4(x, kLog2e);
+      *reinterpret_cast<u32x2*>(Q + k_offset(r, chunk >> 1) + ((chunk & 1) << 3)) =
+          u32x2{pack_h2(x.x, x.y), pack_h2(x.z, x.w)};
+    }
+  }
+  store_tile(0);
+  // Nothing global is in flight when the tile loop starts, so no load issued above can hold
+  // a wait inside it.
+  __builtin_amdgcn_s_waitcnt(kWaitVmem);
+  __syncthreads();
+
+  // Fragment rows are 16*x + col, so the chunk swizzle depends on col only: one per-lane base
+  // per channel step ds (K and Q) or key step ks (V^T), plus compile-time row offsets.
+  const int kq_base[2] = {k_offset(col, grp), k_offset(col, 4 + grp)};
+  const int v_base[2] = {col * 128 + ((grp ^ (col & 7)) << 4),
+                         col * 128 + (((4 + grp) ^ (col & 7)) << 4)};
+  auto q_frag = [&](int qb, int ds) {
+    return *reinterpret_cast<const u32x4*>(Q + kq_base[ds] + qb * 2048);
+  };
+  auto k_frag = [&](const unsigned char* K, int half, int kb2, int ds) {
+    return *reinterpret_cast<const u32x4*>(K + kq_base[ds] + (half * 2 + kb2) * 2048);
+  };
+  auto v_frag = [&](const unsigned char* V, int ks, int db) {
+    return *reinterpret_cast<const u32x4*>(V + v_base[ks] + db * 2048);
+  };
+  // S^T block of 32 keys (half) x 16 queries (qb): acc[kb2][r] = S[key (half*2+kb2)*16 +
+  // grp*4 + r][query qb*16 + col] + init.
+  auto score = [&](const u32x4 (&kf)[2][2], const u32x4 (&qf)[2], float init, f32x4 (&acc)[2]) {
+    const f32x4 c = {init, init, init, init};
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++)
+    for (int kb2 = 0; kb2 < 2; kb2++) acc[kb2] = mfma16x16x32(kf[kb2][0], qf[0], c);
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; kb2++) acc[kb2] = mfma16x16x32(kf[kb2][1], qf[1], acc[kb2]);
+  };
+  auto lane_max = [](const f32x4 (&acc)[2]) {
+    return fmaxf(fmaxf(fmaxf(acc[0][0], acc[0][1]), fmaxf(acc[0][2], acc[0][3])),
+                 fmaxf(fmaxf(acc[1][0], acc[1][1]), fmaxf(acc[1][2], acc[1][3])));
+  };
+
+  if (active) {
+    // The running maximum starts at the exact maximum of the first 32 keys.
+    const unsigned char* K = lds_k[0];
+    u32x4 kf[2][2];
+#pragma unroll
+    for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+      for (int ds = 0; ds < 2; ds++) kf[kb2][ds] = k_frag(K, 0, kb2, ds);
+#pragma unroll
+    for (int qb = 0; qb < 4; qb++) {
+      const u32x4 qf[2] = {q_frag(qb, 0), q_frag(qb, 1)};
+      f32x4 acc[2];
+      score(kf, qf, 0.f, acc);
+      if (T < 32) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
           for (int r = 0; r < 4; r++)
-            if (key0 + kb * 16 + grp * 4 + r >= T) {
-              s[kb][0][r] = kMasked;
-              s[kb][1][r] = kMasked;
-            }
+            if (kb2 * 16 + grp * 4 + r >= T) acc[kb2][r] = kMasked;
       }
+      m[qb] = column_max(lane_max(acc));
+    }
+  }
+
+  // One 64-key tile: 8 work units u = (half u/4, query block u%4). Unit u exponentiates its
+  // scores while the MFMAs of unit u+1's scores run, then issues its PV (and row-sum) MFMAs
+  // while the VALU takes unit u+1's maxima. MASK: keys at or past T exist in this tile.
+  auto tile = [&](auto mask_tag, int j) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int buf = j & 1, key0 = j * 64;
+    const unsigned char* K = lds_k[buf];
+    const unsigned char* V = lds_v[buf];
+    u32x4 kf[2][2][2], vf[2][4];  // [half][kb2][ds], [half][db]
+    u32x4 qf[2][2];               // Q fragments of the next two units, double buffered
+    f32x4 sa[2], sb[2];
+    auto mask_scores = [&](int half, f32x4 (&acc)[2]) {
+      if constexpr (MASK) {
 #pragma unroll
-      for (int qb = 0; qb < 2; qb++) {
-        float mx = kMasked;
+        for (int kb2 = 0; kb2 < 2; kb2++)
 #pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][qb][r]);
-        mx = max_over_rows(mx);
-        const float mn = fmaxf(m[qb], mx);
-        const float alpha = fast_exp2(m[qb] - mn);
-        m[qb] = mn;
-        float sum = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float e = fast_exp2(s[kb][qb][r] - mn);
-            s[kb][qb][r] = e;
-            sum += e;
-          }
-        l[qb] = l[qb] * alpha + sum;
-#pragma unroll
-        for (int db = 0; db < 4; db++) o[db][qb] *= alpha;
+          for (int r = 0; r < 4; r++)
+            if (key0 + (half * 2 + kb2) * 16 + grp * 4 + r >= T) acc[kb2][r] = kMasked;
       }
+    };
+    // Column maximum of a unit's scores and the rescale it may trigger (per query column,
+    // under the exec mask, in place).
+    auto settle = [&](int qb, f32x4 (&acc)[2]) {
+      const float cm = column_max(lane_max(acc));
+      if (cm > kTau) {
+        const float alpha = fast_exp2(-cm);
+        m[qb] += cm;
+        acc[0] -= cm;
+        acc[1] -= cm;
+        lsum[qb] *= alpha;
 #pragma unroll
-      for (int ks = 0; ks < 2; ks++) {
-        const u32x4 pf0 = p_fragment(s[2 * ks][0], s[2 * ks + 1][0]);
-        const u32x4 pf1 = p_fragment(s[2 * ks][1], s[2 * ks + 1][1]);
+        for (int db = 0; db < 4; db++) scale_in_place(o[db][qb], alpha);
+      }
+    };
 #pragma unroll
-        for (int db = 0; db < 4; db++) {
-          const u32x4 vf = vt_fragment(V, db, ks, col, grp);
-          o[db][0] = mfma16x16x32(vf, pf0, o[db][0]);
-          o[db][1] = mfma16x16x32(vf, pf1, o[db][1]);
+    for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+      for (int ds = 0; ds < 2; ds++) kf[0][kb2][ds] = k_frag(K, 0, kb2, ds);
+    qf[0][0] = q_frag(0, 0);
+    qf[0][1] = q_frag(0, 1);
+    qf[1][0] = q_frag(1, 0);
+    qf[1][1] = q_frag(1, 1);
+#pragma unroll
+    for (int db = 0; db < 4; db++) vf[0][db] = v_frag(V, 0, db);
+    score(kf[0], qf[0], -m[0], sa);
+    mask_scores(0, sa);
+    settle(0, sa);
+#pragma unroll
+    for (int u = 0; u < 8; u++) {
+      const int half = u >> 2, qb = u & 3;
+      const int nhalf = (u + 1) >> 2, nqb = (u + 1) & 3;
+      __builtin_amdgcn_sched_barrier(0);
+      if (u == 2) {
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+          for (int ds = 0; ds < 2; ds++) kf[1][kb2][ds] = k_frag(K, 1, kb2, ds);
+      }
+      if (u == 3) {
+#pragma unroll
+        for (int db = 0; db < 4; db++) vf[1][db] = v_frag(V, 1, db);
+      }
+      if (u + 2 < 8) {
+        qf[u & 1][0] = q_frag((u + 2) & 3, 0);
+        qf[u & 1][1] = q_frag((u + 2) & 3, 1);
+      }
+      // Phase A: next unit's S MFMAs interleaved with this unit's exponentials.
+      if (u + 1 < 8) score(kf[nhalf], qf[(u + 1) & 1], -m[nqb], sb);
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) sa[kb2][r] = fast_exp2(sa[kb2][r]);
+      const u32x4 pf = p_fragment(sa[0], sa[1]);
+      // Per-lane partial row sum; the four lanes of a column are added in the epilogue.
+      lsum[qb] += ((sa[0][0] + sa[0][1]) + (sa[0][2] + sa[0][3])) +
+                  ((sa[1][0] + sa[1][1]) + (sa[1][2] + sa[1][3]));
+      if (u + 1 < 8) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+          __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
         }
       }
+      // Phase B: this unit's PV / row-sum MFMAs, then the next unit's maxima.
+#pragma unroll
+      for (int db = 0; db < 4; db++) o[db][qb] = mfma16x16x32(vf[half][db], pf, o[db][qb]);
+      if (u + 1 < 8) {
+        mask_scores(nhalf, sb);
+        settle(nqb, sb);
+        sa[0] = sb[0];
+        sa[1] = sb[1];
+      }
     }
-    if (j + 1 < ntiles) store_tile(buf ^ 1);
+  };
+
+  for (int j = 0; j + 1 < ntiles; j++) {
+    load_tile((j + 1) * 64);
+    if (active) tile(std::false_type{}, j);
+    store_tile((j + 1) & 1);
     __syncthreads();
+  }
+  if (active) {
+    if (T % 64)
+      tile(std::true_type{}, ntiles - 1);
+    else
+      tile(std::false_type{}, ntiles - 1);
   }
 
   if (active) {
+    const OutRows out = out_rows(p, g, h);
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-      const float lt = sum_over_rows(l[qb]);
-      const int t = q0 + qb * 16 + col;
-      f32x4 oq[4] = {o[0][qb], o[1][qb], o[2][qb], o[3][qb]};
-      if (t < T) store_output<GATED, ALIGNED>(p, oq, lt, g, h, t, grp);
+    for (int qb = 0; qb < 4; qb++) {
+      const f32x4 oq[4] = {o[0][qb], o[1][qb], o[2][qb], o[3][qb]};
+      store_output<GATED, ALIGNED>(out, oq, sum_over_rows(lsum[qb]), q0 + qb * 16 + col, grp);
     }
   }
 }
@@ -291,9 +511,12 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   const int pr = active ? prob : 0;
   const int h = pr % p.heads, g = pr / p.heads;
   const int T = p.tokens;
-  const float* qg = p.q + (long)g * T * p.ldq + h * 64;
-  const float* kg = p.k + (long)g * T * p.ldk + h * 64;
-  const float* vg = p.v + (long)g * T * p.ldv + h * 64;
+  const unsigned ldq4 = (unsigned)p.ldq * 4, ldk4 = (unsigned)p.ldk * 4,
+                 ldv4 = (unsigned)p.ldv * 4;
+  const rsrc_t qr = make_rsrc(p.q + (long)g * T * p.ldq + h * 64, (unsigned)(T - 1) * ldq4 + 256);
+  const rsrc_t kr = make_rsrc(p.k + (long)g * T * p.ldk + h * 64, (unsigned)(T - 1) * ldk4 + 256);
+  const rsrc_t vr = make_rsrc(p.v + (long)g * T * p.ldv + h * 64, (unsigned)(T - 1) * ldv4 + 256);
+  const rsrc_t tr = make_rsrc(ROPE ? p.rope : p.q, ROPE ? (unsigned)T * 1024 : 0);
   unsigned char* vt = lds_v[wave];
 
   if (active) {
@@ -302,14 +525,11 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
 #pragma unroll
     for (int it = 0; it < 4; it++) {
       const int kq = grp + 4 * it;
-      float4 vr[4];
+      float4 v4[4];
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int t = kq * 4 + r;
-        vr[r] = t < T ? load4<ALIGNED>(vg + (long)t * p.ldv + col * 4)
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-      store_vt_block(vt, vr, kq, col);
+      for (int r = 0; r < 4; r++)
+        v4[r] = bload4<ALIGNED>(vr, (unsigned)(kq * 4 + r) * ldv4 + col * 16);
+      store_vt_block(vt, v4, kq, col);
     }
   }
   __syncthreads();
@@ -321,8 +541,10 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   for (int kb = 0; kb < 4; kb++)
 #pragma unroll
     for (int ds = 0; ds < 2; ds++)
-      kf[kb][ds] = load_fragment<ROPE, ALIGNED>(kg, p.ldk, kb * 16 + col, T, ds * 32 + grp * 8,
-                                                p.rope, 2, 1.0f);
+      kf[kb][ds] = load_fragment<ROPE, ALIGNED>(kr, ldk4, tr, T, kb * 16 + col, ds * 32 + grp * 8,
+                                                2, 1.0f);
+  const OutRows out = out_rows(p, g, h);
+  const u32x4 ones = {kOnesH2, kOnesH2, kOnesH2, kOnesH2};
 
 #pragma unroll
   for (int qp = 0; qp < 2; qp++) {
@@ -331,13 +553,13 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
     for (int qb = 0; qb < 2; qb++)
 #pragma unroll
       for (int ds = 0; ds < 2; ds++)
-        qf[qb][ds] = load_fragment<ROPE, ALIGNED>(qg, p.ldq, (qp * 2 + qb) * 16 + col, T,
-                                                  ds * 32 + grp * 8, p.rope, 0, kLog2e);
+        qf[qb][ds] = load_fragment<ROPE, ALIGNED>(qr, ldq4, tr, T, (qp * 2 + qb) * 16 + col,
+                                                  ds * 32 + grp * 8, 0, kLog2e);
     f32x4 s[4][2];
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) {
-      s[kb][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      s[kb][1] = s[kb][0];
+      s[kb][0] = zero4();
+      s[kb][1] = zero4();
 #pragma unroll
       for (int ds = 0; ds < 2; ds++) {
         s[kb][0] = mfma16x16x32(kf[kb][ds], qf[0][ds], s[kb][0]);
@@ -354,7 +576,7 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
             s[kb][1][r] = kMasked;
           }
     }
-    float l[2];
+    u32x4 pf[2][2];
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
       float mx = kMasked;
@@ -363,39 +585,34 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
 #pragma unroll
         for (int r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][qb][r]);
       mx = max_over_rows(mx);
-      float sum = 0.f;
 #pragma unroll
       for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float e = fast_exp2(s[kb][qb][r] - mx);
-          s[kb][qb][r] = e;
-          sum += e;
-        }
-      l[qb] = sum_over_rows(sum);
+        for (int r = 0; r < 4; r++) s[kb][qb][r] = fast_exp2(s[kb][qb][r] - mx);
+      pf[0][qb] = p_fragment(s[0][qb], s[1][qb]);
+      pf[1][qb] = p_fragment(s[2][qb], s[3][qb]);
     }
-    f32x4 o[4][2];
+    f32x4 o[4][2], lsum[2] = {zero4(), zero4()};
 #pragma unroll
     for (int db = 0; db < 4; db++) {
-      o[db][0] = f32x4{0.f, 0.f, 0.f, 0.f};
-      o[db][1] = o[db][0];
+      o[db][0] = zero4();
+      o[db][1] = zero4();
     }
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-      const u32x4 pf0 = p_fragment(s[2 * ks][0], s[2 * ks + 1][0]);
-      const u32x4 pf1 = p_fragment(s[2 * ks][1], s[2 * ks + 1][1]);
 #pragma unroll
       for (int db = 0; db < 4; db++) {
         const u32x4 vf = vt_fragment(vt, db, ks, col, grp);
-        o[db][0] = mfma16x16x32(vf, pf0, o[db][0]);
-        o[db][1] = mfma16x16x32(vf, pf1, o[db][1]);
+        o[db][0] = mfma16x16x32(vf, pf[ks][0], o[db][0]);
+        o[db][1] = mfma16x16x32(vf, pf[ks][1], o[db][1]);
       }
+      lsum[0] = mfma16x16x32(ones, pf[ks][0], lsum[0]);
+      lsum[1] = mfma16x16x32(ones, pf[ks][1], lsum[1]);
     }
 #pragma unroll
     for (int qb = 0; qb < 2; qb++) {
-      const int t = (qp * 2 + qb) * 16 + col;
-      f32x4 oq[4] = {o[0][qb], o[1][qb], o[2][qb], o[3][qb]};
-      if (t < T) store_output<GATED, ALIGNED>(p, oq, l[qb], g, h, t, grp);
+      const f32x4 oq[4] = {o[0][qb], o[1][qb], o[2][qb], o[3][qb]};
+      store_output<GATED, ALIGNED>(out, oq, lsum[qb][0], (qp * 2 + qb) * 16 + col, grp);
     }
   }
 }
@@ -408,10 +625,10 @@ static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED>), dim3((problems + 3) / 4),
                        dim3(256), 0, stream, p, problems);
   } else {
-    const int qblocks = (T + 127) / 128;
+    const int qblocks = (T + kTimeQueries - 1) / kTimeQueries;
     const int total = p.groups * p.heads * qblocks;
-    hipLaunchKernelGGL((attention_time_kernel<GATED, ROPE, ALIGNED>), dim3(total), dim3(256), 0,
-                       stream, p, qblocks, total);
+    hipLaunchKernelGGL((attention_time_kernel<GATED, ROPE, ALIGNED>), dim3(total),
+                       dim3(kTimeWaves * 64), 0, stream, p, qblocks, total);
   }
   return hipGetLastError();
 }
