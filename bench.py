@@ -36,6 +36,17 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def profiled_traffic(workload: str):
+    """HBM bytes per launch of the attention kernel from the committed counter summary
+    (profiles/attention_<workload>_*.md: FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"attention_{workload}_*.md"))):
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    return None
+
+
 def cpu_threads() -> int:
     try:
         n = len(os.sched_getaffinity(0))
@@ -71,8 +82,8 @@ def cpu_baseline(q, k, v, table, gpu_out, budget_s: float = 12.0) -> dict:
                             threads=threads)
     probe = time.perf_counter() - t0
     groups = int(min(G, max(g1, g1 * budget_s / 3.0 / max(probe, 1e-3))))
-    groups = max(threads, groups // threads * threads) if groups >= threads else groups
-    groups = min(groups, G)
+    if groups < G and groups >= threads:
+        groups = groups // threads * threads
     qs, ks, vs = sample(groups)
     times, out = [], None
     for _ in range(3):
@@ -95,6 +106,26 @@ def cpu_baseline(q, k, v, table, gpu_out, budget_s: float = 12.0) -> dict:
     }
 
 
+def copy_calibration(torch, dev, elements: int, steps: int) -> int:
+    """A plain float32 device copy of `elements` values (read once, written once) repeated
+    `steps` times; prints the bytes moved and the rate."""
+    src = torch.ones(elements, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    print(json.dumps({"copy_bytes_read": elements * 4, "copy_bytes_written": elements * 4,
+                      "ms_per_copy": round(ms, 4),
+                      "GB/s": round(2 * elements * 4 / ms / 1e6, 1)}), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -102,6 +133,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", choices=["time", "band"], default="time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="time a plain device copy of the workload's I/O size instead; its "
+                         "FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic figures")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -123,6 +157,8 @@ def main() -> int:
     G, T, H, D = shape
     log(f"generating q, k, v {shape} on the GPU")
     q, k, v = (W.normal_torch(shape, s, 1.0 / 8.0, device=dev) for s in (1, 2, 3))
+    if args.copy_calibration:
+        return copy_calibration(torch, dev, G * T * H * D * 2, args.steps)
     table_np = W.axis_rope_packed(W.rope_freqs(), T)
     table = torch.from_numpy(table_np).to(dev)
     torch.cuda.synchronize()
@@ -154,11 +190,12 @@ def main() -> int:
         achieved = flops / (kernel_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
-                    "traffic": None}
+                    "traffic": profiled_traffic("time")}
     else:
         achieved = io_bytes / (kernel_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None}
+                    "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": profiled_traffic("band")}
     result = {
         "metric": "fused attn TFLOP/s (% MFMA peak)",
         "value": round(value, 3),

@@ -1,0 +1,89 @@
+"""Inputs of the golden fixtures, regenerated from closed forms (shared by make_golden.py and
+the tests). Mirrors the reference's test inputs: `wave` is tests/cuda_contracts.rs:183-189."""
+from __future__ import annotations
+
+import numpy as np
+
+from ancha_amd import workload as W
+
+# tests/cuda_contracts.rs:199-204: partial tiles, a single token, a strided layout.
+ATTENTION_SHAPES = [(2, 1, 1), (3, 63, 2), (2, 65, 1), (1, 130, 3)]
+
+# tests/cuda_contracts.rs:253-295: the GEMM epilogue case.
+LINEAR_GROUPS, LINEAR_TOKENS, LINEAR_K, LINEAR_HEADS = 3, 70, 64, 2
+LINEAR_WIDTH = LINEAR_HEADS * 64
+LINEAR_GELU_ROWS = np.arange(0, 210, 7)          # 30 of the 210 rows
+LINEAR_ROTARY_ROWS = np.arange(70, 140)          # one whole group: every token position
+
+# Single-group slices of the two production shapes (seeds 1/2/3, N(0,1)/8, RoPE on load).
+SLICES = {
+    "time": ((1, 801, 8, 64), np.r_[np.arange(0, 768, 8), np.arange(768, 801)], [0, 5]),
+    "band": ((1, 60, 8, 64), np.arange(60), [0, 7]),
+}
+
+# A small RoFormer block (dim 128, 2 heads, FF 512, output norm) on [3, 37, 128].
+LAYER_DIM, LAYER_HEADS, LAYER_HIDDEN, LAYER_SHAPE = 128, 2, 512, (3, 37, 128)
+
+
+def wave(shape, shift):
+    n = int(np.prod(shape))
+    i = np.arange(n, dtype=np.float32)
+    return np.tanh(np.sin(i * np.float32(0.731) + np.float32(shift)) * np.float32(1.7)).astype(
+        np.float32).reshape(shape)
+
+
+def checksum(*arrays):
+    """Float64 sums of each input and of its elements weighted by position (order-sensitive)."""
+    out = []
+    for a in arrays:
+        a = np.asarray(a, np.float64).ravel()
+        out += [a.sum(), (a * (np.arange(a.size) % 97 + 1)).sum()]
+    return np.array(out)
+
+
+def attention_case(groups, tokens, heads):
+    """q (pre-scaled by 1/8), k, v [G, T, H, 64]; gates [G, T, H]; the packed
+    q | k | v | gates | 5 zero columns layout of the same values."""
+    q = wave((groups, tokens, heads, 64), 0.1) * np.float32(0.4) * np.float32(0.125)
+    k = wave((groups, tokens, heads, 64), 1.3)
+    v = wave((groups, tokens, heads, 64), 2.9)
+    gates = wave((groups, tokens, heads), 4.4) * np.float32(3.0)
+    flat = lambda a: a.reshape(groups, tokens, heads * 64)
+    packed = np.concatenate([flat(q), flat(k), flat(v), gates,
+                             np.zeros((groups, tokens, 5), np.float32)], axis=2)
+    return q, k, v, gates, packed
+
+
+def linear_case():
+    rows, m = LINEAR_GROUPS * LINEAR_TOKENS, 3 * LINEAR_WIDTH
+    x = wave((rows, LINEAR_K), 0.3)
+    w = wave((LINEAR_K, m), 1.1) * np.float32(0.1)
+    b = wave((m,), 2.2)
+    r = wave((rows, m), 3.3)
+    freqs = (np.float32(10000.0) ** (-np.arange(32, dtype=np.float32) / np.float32(32.0))).astype(
+        np.float32)
+    return x, w, b, r, W.axis_rope_packed(freqs, LINEAR_TOKENS), freqs
+
+
+def slice_case(shape):
+    q, k, v = W.attention_inputs(shape)
+    freqs = W.rope_freqs()
+    return q, k, v, W.axis_rope_packed(freqs, shape[1]), freqs
+
+
+def layer_case():
+    shapes = {
+        "attn_gamma": (LAYER_DIM,), "to_qkv": (3 * LAYER_HEADS * 64, LAYER_DIM),
+        "to_gates": (LAYER_HEADS, LAYER_DIM), "to_gates_bias": (LAYER_HEADS,),
+        "to_out": (LAYER_DIM, LAYER_HEADS * 64), "ff_gamma": (LAYER_DIM,),
+        "ff_in": (LAYER_HIDDEN, LAYER_DIM), "ff_in_bias": (LAYER_HIDDEN,),
+        "ff_out": (LAYER_DIM, LAYER_HIDDEN), "ff_out_bias": (LAYER_DIM,),
+        "output_gamma": (LAYER_DIM,),
+    }
+    w = {"heads": LAYER_HEADS, "freqs": W.rope_freqs()}
+    for i, (name, shape) in enumerate(sorted(shapes.items())):
+        if name.endswith("gamma"):
+            w[name] = 1.0 + W.normal(shape, W.SEED_WEIGHTS + i, 0.1)
+        else:
+            w[name] = W.normal(shape, W.SEED_WEIGHTS + i, 0.02)
+    return w, W.normal(LAYER_SHAPE, 4)

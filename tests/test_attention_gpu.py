@@ -175,3 +175,23 @@ def test_runs_on_a_side_stream(gpu):
         got = fused.attention(q, k, v)
     torch.cuda.current_stream().wait_stream(s)
     assert torch.equal(ref, got)
+
+
+def test_kernels_match_golden_fixtures(gpu):
+    from tests.golden import cases as C
+    import os
+    here = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+    slices = np.load(os.path.join(here, "production_slices.npz"), allow_pickle=False)
+    for name, (shape, rows, heads) in C.SLICES.items():
+        q, k, v, table, _ = C.slice_case(shape)
+        got = fused.attention(dev(q, gpu), dev(k, gpu), dev(v, gpu), rope=dev(table, gpu))
+        err = np.abs(got.cpu().numpy()[0][np.ix_(rows, heads)] - slices[name]).max()
+        report(f"golden {name} slice", err)
+        assert err < TOL
+    cases = np.load(os.path.join(here, "attention_cases.npz"), allow_pickle=False)
+    for shape in C.ATTENTION_SHAPES:
+        q, k, v, gates, packed = C.attention_case(*shape)
+        got = fused.gated_attention(dev(packed, gpu), shape[2])
+        err = np.abs(got.cpu().numpy() - cases["gated_" + "x".join(map(str, shape))]).max()
+        report(f"golden gated {shape}", err)
+        assert err < TOL
