@@ -37,7 +37,13 @@ SIGNATURES = {
     "ancha_hip_gated_attention": (_int, [_p, _sz, _sz, _sz, _sz, _p, _p, _p]),
     "ancha_hip_linear": (_int, [_p, _sz, _sz, _sz, _p, _sz, _p, _int, _p, _sz, _sz, _p, _p, _p]),
     "ancha_hip_linear_supported": (_int, [_sz, _sz]),
+    "ancha_hip_norm_linear": (_int, [_p, _sz, _sz, _sz, _p, _sz, _p, _int, _p, _sz, _sz, _p, _p,
+                                     _p]),
     "ancha_hip_unit_norm": (_int, [_p, _sz, _sz, _sz, _p, _p, _p]),
+    "ancha_hip_block_create": (_int, [_sz, _sz, _sz] + [_p] * 11 + [ctypes.POINTER(_p)]),
+    "ancha_hip_block_workspace": (_sz, [_p, _sz]),
+    "ancha_hip_block_forward": (_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p, _p]),
+    "ancha_hip_block_destroy": (None, [_p]),
     "ancha_hip_check": (_int, []),
     "ancha_hip_last_error": (ctypes.c_char_p, []),
 }

@@ -80,9 +80,97 @@ int run_attention(ancha::AttnParams& p, size_t groups, size_t tokens, size_t hea
   return ANCHA_HIP_OK;
 }
 
+// fused::linear's shape contract (fused/mod.rs:100-127) plus the limits of 32-bit buffer
+// offsets inside one 128-row tile.
+int run_linear(const float* x, size_t n, size_t k, size_t ldx, const float* w, size_t m,
+               const float* bias, int gelu, const float* rope, size_t tokens, size_t width,
+               const float* residual, float* out, bool norm, hipStream_t stream,
+               const char* name) {
+  if (const int s = sticky()) return s;
+  const std::string who(name);
+  if (k == 0 || k % 8 != 0 || m == 0) return fail(ANCHA_HIP_UNSUPPORTED, who + ": k % 8 != 0 or empty");
+  const bool epilogue = bias || gelu || rope || residual;
+  if (epilogue && m % 128 != 0)
+    return fail(ANCHA_HIP_UNSUPPORTED, who + ": an epilogue needs m % 128 == 0");
+  if (rope && (tokens == 0 || n % tokens != 0 || width % 64 != 0 || 2 * width > m))
+    return fail(ANCHA_HIP_UNSUPPORTED, who + ": rotary shape (tokens, width) does not fit");
+  if (ldx < k) return fail(ANCHA_HIP_INVALID, who + ": ldx < k");
+  if (n == 0) return ANCHA_HIP_OK;
+  if (!x || !w || !out) return fail(ANCHA_HIP_INVALID, who + ": null tensor");
+  const size_t kLimit = size_t(1) << 31;
+  const size_t tiles = ((n + 127) / 128) * ((m + 127) / 128);
+  if (n > kIntMax || tiles > kIntMax || (k + 64) * m * 4 >= kLimit * 2 || 128 * ldx * 4 >= kLimit ||
+      128 * m * 4 >= kLimit || (rope && (tokens > kIntMax || tokens * 1024 >= kLimit * 2)))
+    return fail(ANCHA_HIP_UNSUPPORTED, who + ": operand exceeds the 32-bit buffer range");
+  if (!device_is_gfx950()) return fail(ANCHA_HIP_UNSUPPORTED, who + ": not a gfx950 device");
+  ancha::LinearParams p{};
+  p.x = x;
+  p.w = w;
+  p.bias = bias;
+  p.rope = rope;
+  p.residual = residual;
+  p.out = out;
+  p.ldx = static_cast<long>(ldx);
+  p.n = static_cast<int>(n);
+  p.k = static_cast<int>(k);
+  p.m = static_cast<int>(m);
+  p.tokens = rope ? static_cast<int>(tokens) : 1;
+  p.width = rope ? static_cast<int>(width) : 0;
+  p.gelu = gelu ? 1 : 0;
+  p.norm = norm ? 1 : 0;
+  const bool aligned = aligned16(x) && aligned16(w) && aligned16(out) &&
+                       (!bias || aligned16(bias)) && (!residual || aligned16(residual)) &&
+                       (!rope || aligned16(rope)) && ldx % 4 == 0 && m % 4 == 0;
+  const hipError_t e = ancha::launch_linear(p, aligned, stream);
+  if (e != hipSuccess) return hip_fail(e, name);
+  return ANCHA_HIP_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+int ancha_hip_linear_supported(size_t k, size_t m) {
+  return k > 0 && k % 8 == 0 && m > 0 && m % 128 == 0 ? 1 : 0;
+}
+
+int ancha_hip_linear(const float* x, size_t n, size_t k, size_t ldx, const float* w, size_t m,
+                     const float* bias, int gelu, const float* rope, size_t tokens, size_t width,
+                     const float* residual, float* out, hipStream_t stream) {
+  return run_linear(x, n, k, ldx, w, m, bias, gelu, rope, tokens, width, residual, out, false,
+                    stream, "ancha_hip_linear");
+}
+
+int ancha_hip_norm_linear(const float* x, size_t n, size_t k, size_t ldx, const float* w,
+                          size_t m, const float* bias, int gelu, const float* rope,
+                          size_t tokens, size_t width, const float* residual, float* out,
+                          hipStream_t stream) {
+  return run_linear(x, n, k, ldx, w, m, bias, gelu, rope, tokens, width, residual, out, true,
+                    stream, "ancha_hip_norm_linear");
+}
+
+int ancha_hip_unit_norm(const float* x, size_t rows, size_t dim, size_t ldx, const float* scale,
+                        float* out, hipStream_t stream) {
+  if (const int s = sticky()) return s;
+  if (ldx < dim) return fail(ANCHA_HIP_INVALID, "ancha_hip_unit_norm: ldx < dim");
+  if (rows == 0 || dim == 0) return ANCHA_HIP_OK;
+  if (!x || !out) return fail(ANCHA_HIP_INVALID, "ancha_hip_unit_norm: null tensor");
+  if (rows > kIntMax || dim * 4 >= (size_t(1) << 31))
+    return fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_unit_norm: too many rows or columns");
+  if (!device_is_gfx950()) return fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_unit_norm: not a gfx950 device");
+  ancha::NormParams p{};
+  p.x = x;
+  p.scale = scale;
+  p.out = out;
+  p.ldx = static_cast<long>(ldx);
+  p.rows = static_cast<int>(rows);
+  p.dim = static_cast<int>(dim);
+  const bool aligned = aligned16(x) && aligned16(out) && (!scale || aligned16(scale)) &&
+                       dim % 4 == 0 && ldx % 4 == 0;
+  const hipError_t e = ancha::launch_unit_norm(p, aligned, stream);
+  if (e != hipSuccess) return hip_fail(e, "ancha_hip_unit_norm");
+  return ANCHA_HIP_OK;
+}
 
 int ancha_hip_available(void) {
   int count = 0;

@@ -21,4 +21,39 @@ struct AttnParams {
 // `aligned`: every float4 access is 16-byte aligned (base pointers and row strides).
 hipError_t launch_attention(const AttnParams& p, bool aligned, hipStream_t stream);
 
+// out = epilogue(x . w): x [n, k] (row stride ldx), w [k, m] row-major (the reference's
+// [in, out] Linear layout), out [n, m] contiguous. Epilogue, in order: optional input row norm
+// (the product of row r scaled by 1 / max(||x_r||, 1e-12)), bias [m], erf-GELU, interleaved
+// rotary on columns [0, 2*width) (queries then keys of token r % tokens, packed [4, tokens, 64]
+// table), residual [n, m] contiguous.
+struct LinearParams {
+  const float* x;
+  const float* w;
+  const float* bias;      // or null
+  const float* rope;      // or null
+  const float* residual;  // or null (may alias out)
+  float* out;
+  long ldx;
+  int n, k, m;
+  int tokens, width;
+  int gelu;
+  int norm;
+};
+
+// `aligned`: x, w, out (and bias / residual / rope when present) are 16-byte aligned, ldx and m
+// are multiples of 4.
+hipError_t launch_linear(const LinearParams& p, bool aligned, hipStream_t stream);
+
+// out[r] = x[r] / max(||x[r]||, 1e-12) * scale (scale [dim] or null): x [rows, dim] with row
+// stride ldx, out [rows, dim] contiguous; out may alias x when ldx == dim.
+struct NormParams {
+  const float* x;
+  const float* scale;
+  float* out;
+  long ldx;
+  int rows, dim;
+};
+
+hipError_t launch_unit_norm(const NormParams& p, bool aligned, hipStream_t stream);
+
 }  // namespace ancha

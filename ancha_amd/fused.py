@@ -113,3 +113,82 @@ class Epilogue:
     def empty(self) -> bool:
         return (self.bias is None and not self.gelu and self.rotary is None
                 and self.residual is None)
+
+
+def linear_supported(k: int, m: int) -> bool:
+    """fused/mod.rs:83-85: the 128-wide tile covers [n, k].[k, m] without padding."""
+    return k > 0 and k % 8 == 0 and m > 0 and m % 128 == 0
+
+
+def _matrix(t: torch.Tensor, name: str) -> torch.Tensor:
+    if t.dim() != 2 or t.dtype != torch.float32 or not t.is_cuda:
+        raise ValueError(f"{name} must be a float32 CUDA matrix")
+    return t if t.stride(1) == 1 else t.contiguous()
+
+
+def _linear(x: torch.Tensor, weight: torch.Tensor, epilogue: Epilogue,
+            norm: bool) -> Optional[torch.Tensor]:
+    n, k = x.shape
+    rows, m = weight.shape
+    if rows != k or k == 0 or k % 8 != 0 or m == 0:
+        return None
+    if m % 128 != 0 and not epilogue.empty():
+        return None
+    tokens = width = 0
+    table = None
+    if epilogue.rotary is not None:
+        table, width = epilogue.rotary
+        four, tokens, dim = table.shape
+        if four != 4 or dim != ATTENTION_HEAD_DIM or n % tokens != 0 or width % 64 != 0 \
+                or 2 * width > m:
+            return None
+        table = table.contiguous()
+    residual = epilogue.residual
+    if residual is not None:
+        if tuple(residual.shape) != (n, m):
+            return None
+        residual = residual.contiguous()
+    if not x.is_cuda or not available():
+        return None
+    x = _matrix(x, "x")
+    w = _matrix(weight, "weight").contiguous()
+    bias = None if epilogue.bias is None else epilogue.bias.contiguous()
+    out = torch.empty((n, m), device=x.device, dtype=torch.float32)
+    fn = _native.lib().ancha_hip_norm_linear if norm else _native.lib().ancha_hip_linear
+    rc = fn(x.data_ptr(), n, k, x.stride(0), w.data_ptr(), m, _ptr(bias), int(epilogue.gelu),
+            _ptr(table), tokens, width, _ptr(residual), out.data_ptr(), _stream())
+    return out if _native.check(rc) else None
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor,
+           epilogue: Optional[Epilogue] = None) -> Optional[torch.Tensor]:
+    """fused/mod.rs:100-176: x [n, k] . weight [k, m] (Burn Linear layout) followed by the
+    epilogue (bias -> erf-GELU -> rotary -> residual); [n, m] or None when the shape or the
+    epilogue does not fit (k % 8, m % 128 with an epilogue, rotary shape, residual shape)."""
+    return _linear(x, weight, epilogue or Epilogue(), norm=False)
+
+
+def norm_linear(x: torch.Tensor, weight: torch.Tensor,
+                epilogue: Optional[Epilogue] = None) -> Optional[torch.Tensor]:
+    """``linear(unit_norm(x), weight, epilogue)`` in one kernel (the row norm scales the
+    product), the call pattern of Transformer::forward_kernels (roformer.rs:477-485, :497-505)."""
+    return _linear(x, weight, epilogue or Epilogue(), norm=True)
+
+
+def unit_norm(x: torch.Tensor, scale: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """roformer.rs:16-24 (and SourceNorm::forward :51-53 with scale = sqrt(dim)*gamma):
+    x / max(||x||_2, 1e-12) over the last axis, times ``scale``."""
+    if x.dtype != torch.float32 or not x.is_cuda:
+        raise ValueError("unit_norm takes a float32 CUDA tensor")
+    if not available():
+        raise RuntimeError("the gfx950 kernels cannot run on this device")
+    dim = x.shape[-1]
+    flat = x.reshape(-1, dim)
+    if flat.stride(1) != 1:
+        flat = flat.contiguous()
+    out = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    s = None if scale is None else scale.contiguous()
+    rc = _native.lib().ancha_hip_unit_norm(flat.data_ptr(), flat.shape[0], dim, flat.stride(0),
+                                           _ptr(s), out.data_ptr(), _stream())
+    _native.check(rc)
+    return out

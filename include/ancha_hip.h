@@ -68,6 +68,76 @@ int ancha_hip_attention(const float *q, const float *k, const float *v, size_t g
 int ancha_hip_gated_attention(const float *packed, size_t groups, size_t tokens, size_t columns,
                               size_t heads, const float *rope, float *out, hipStream_t stream);
 
+/* Whether the projection GEMM covers [n, k].[k, m] with its full 128-column tile:
+ * k % 8 == 0 and m % 128 == 0 (both > 0). Other positive m still run as bare products.
+ * Replaces `fused::linear_supported(k, m)` (fused/mod.rs:83-85). */
+int ancha_hip_linear_supported(size_t k, size_t m);
+
+/* out [n, m] = epilogue(x . w): x [n, k] with row stride ldx, w [k, m] row-major (the
+ * reference's Burn `Linear` [in, out] layout), out [n, m] contiguous. Epilogue applied in the
+ * reference's order (fused/gemm.rs:46-82): bias [m] (or NULL); erf-GELU if gelu != 0; rotary if
+ * rope != NULL: the packed [4, tokens, 64] AxisRope table, columns [0, width) of row r rotated
+ * as queries and [width, 2*width) as keys of token r % tokens; residual [n, m] contiguous (or
+ * NULL; may alias out). fp16 MFMA operands, fp32 accumulation.
+ * Returns ANCHA_HIP_UNSUPPORTED where the reference returns `None`: k == 0, k % 8 != 0, m == 0;
+ * an epilogue with m % 128 != 0; rotary with tokens == 0, n % tokens != 0, width % 64 != 0 or
+ * 2*width > m.
+ * Replaces `fused::linear(x, weight, Epilogue{bias, gelu, rotary, residual})`
+ * (fused/mod.rs:58-176; kernel fused/gemm.rs:86-311). */
+int ancha_hip_linear(const float *x, size_t n, size_t k, size_t ldx, const float *w, size_t m,
+                     const float *bias, int gelu, const float *rope, size_t tokens, size_t width,
+                     const float *residual, float *out, hipStream_t stream);
+
+/* ancha_hip_linear applied to unit_norm(x) without materialising it: each row's product is
+ * scaled by 1 / max(||x_r||_2, 1e-12) before the epilogue. Same arguments and return codes.
+ * Replaces the pair `fused::linear(&unit_norm(x), weight, epilogue)` of
+ * Transformer::forward_kernels (roformer.rs:477-485 and :497-505; unit_norm :16-24). */
+int ancha_hip_norm_linear(const float *x, size_t n, size_t k, size_t ldx, const float *w,
+                          size_t m, const float *bias, int gelu, const float *rope,
+                          size_t tokens, size_t width, const float *residual, float *out,
+                          hipStream_t stream);
+
+/* out[r] = x[r] / max(||x[r]||_2, 1e-12) * scale: x [rows, dim] with row stride ldx, scale
+ * [dim] or NULL, out [rows, dim] contiguous (may alias x when ldx == dim).
+ * Replaces `unit_norm` (roformer.rs:16-24) and, with scale = sqrt(dim)*gamma,
+ * `SourceNorm::forward` (roformer.rs:43-54). */
+int ancha_hip_unit_norm(const float *x, size_t rows, size_t dim, size_t ldx, const float *scale,
+                        float *out, hipStream_t stream);
+
+/* One RoFormer transformer block on the kernels above (opaque handle, device-resident
+ * packed weights). */
+typedef struct ancha_hip_block ancha_hip_block;
+
+/* Load-time packing of one block from host fp32 weights in PyTorch nn.Linear layout
+ * ([out, in]): attn_gamma [dim], to_qkv [3*heads*64, dim], to_gates [heads, dim],
+ * to_gates_bias [heads], to_out [dim, heads*64], ff_gamma [dim], ff_in [hidden, dim],
+ * ff_in_bias [hidden], ff_out [dim, hidden], ff_out_bias [dim], output_gamma [dim] or NULL.
+ * sqrt(dim)*gamma folds into the following projections' input rows and q | k | v | gates are
+ * packed side by side, zero-padded to a multiple of 128 columns. Allocates the device weights
+ * on the current device. UNSUPPORTED when a projection shape fails ancha_hip_linear_supported.
+ * Replaces `Transformer::load` + `Attention::load` (roformer.rs:381-409, :205-244; folding
+ * weights.rs:149-176). */
+int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float *attn_gamma,
+                           const float *to_qkv, const float *to_gates,
+                           const float *to_gates_bias, const float *to_out,
+                           const float *ff_gamma, const float *ff_in, const float *ff_in_bias,
+                           const float *ff_out, const float *ff_out_bias,
+                           const float *output_gamma, ancha_hip_block **block);
+
+/* Device bytes of the workspace ancha_hip_block_forward needs for `rows` = groups*tokens. */
+size_t ancha_hip_block_workspace(const ancha_hip_block *block, size_t rows);
+
+/* y = block(x): x, out [groups, tokens, dim] contiguous (out may alias x); rope the packed
+ * [4, tokens, 64] AxisRope table of this axis; workspace >= ancha_hip_block_workspace bytes.
+ * x + gated attention(unit_norm x) -> x + FF(unit_norm x) -> optional output norm, on the
+ * packed-projection path with RoPE in the QKV epilogue. Allocates nothing.
+ * Replaces `Transformer::forward_kernels` (roformer.rs:464-520). */
+int ancha_hip_block_forward(const ancha_hip_block *block, const float *x, size_t groups,
+                            size_t tokens, const float *rope, void *workspace,
+                            size_t workspace_bytes, float *out, hipStream_t stream);
+
+void ancha_hip_block_destroy(ancha_hip_block *block);
+
 /* Sticky device-failure check: 0, or the first HIP error (< 0) any call has met.
  * Replaces `device::check()` (src/device.rs:30-41) for this path. */
 int ancha_hip_check(void);

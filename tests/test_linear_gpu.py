@@ -1,0 +1,195 @@
+"""Parity of the gfx950 projection GEMM, row norm and RoFormer block (through the C ABI) with
+the oracle.
+
+GEMM tolerance: the kernel rounds x and w to fp16 (relative error <= 2^-11 each) and
+accumulates in fp32, so |got - exact| <= 2^-10 * sum_k |x_ik| |w_kj| (+ fp32 accumulation,
+~1e-6 relative). Tests assert that bound per element, times the Lipschitz constant of the
+epilogue that follows (1.13 for erf-GELU, sqrt(2) for a pair rotation, 1 for bias/residual).
+Attention-block outputs are held to the path's 2e-3 max-abs bound.
+Cases follow tests/cuda_contracts.rs:253-297 of the reference (the GEMM epilogues) and
+Transformer::forward_kernels (roformer.rs:464-520) for the block.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from ancha_amd import fused, roformer
+from ancha_amd import workload as W
+from tests.golden import cases as C
+
+pytestmark = pytest.mark.gpu
+
+EPS16 = 2.0 ** -10
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def dev(a, gpu):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(gpu)
+
+
+def bound(x, w, lipschitz=1.0):
+    return lipschitz * (EPS16 * (np.abs(x).astype(np.float64) @ np.abs(w).astype(np.float64))
+                        + 1e-5)
+
+
+def check(name, got, want, tol):
+    err = np.abs(got.astype(np.float64) - want)
+    ratio = float((err / tol).max())
+    print(f"{name}: max|diff| {err.max():.3e}, worst diff/bound {ratio:.3f}", flush=True)
+    assert ratio <= 1.0, name
+
+
+def test_reference_epilogue_cases(gpu):
+    x, w, b, r, table, _ = C.linear_case()
+    tokens, width = C.LINEAR_TOKENS, C.LINEAR_WIDTH
+    X, Wt, B, R = dev(x, gpu), dev(w, gpu), dev(b, gpu), dev(r, gpu)
+    ep = fused.Epilogue(bias=B, gelu=True, residual=R)
+    got = fused.linear(X, Wt, ep).cpu().numpy()
+    want = O.linear(x, w, bias=b, gelu=True, residual=r)
+    check("bias+GELU+residual", got, want, bound(x, w, 1.13))
+    ep = fused.Epilogue(bias=B, rotary=(dev(table, gpu), width))
+    got = fused.linear(X, Wt, ep).cpu().numpy()
+    want = O.linear(x, w, bias=b, rope=table, tokens=tokens, width=width)
+    check("bias+rotary", got, want, bound(x, w, 1.42))
+    # The committed golden rows (independent float64 restatement).
+    f = np.load(os.path.join(GOLDEN, "linear_epilogue.npz"), allow_pickle=False)
+    check("rotary golden rows", got[C.LINEAR_ROTARY_ROWS], f["rotary_rows"],
+          bound(x, w, 1.42)[C.LINEAR_ROTARY_ROWS] + 1e-6)
+
+
+@pytest.mark.parametrize("n,k,m,ldx", [(1000, 384, 1664, 384), (77, 1536, 384, 1536),
+                                       (130, 512, 384, 515), (5, 8, 128, 8)])
+def test_shapes_and_strides(gpu, n, k, m, ldx):
+    base = W.normal((n, ldx), 11, 1.0)
+    x = base[:, :k]
+    w = W.normal((k, m), 12, 0.05)
+    b = W.normal((m,), 13, 0.1)
+    r = W.normal((n, m), 14, 1.0)
+    X = dev(base, gpu)[:, :k]
+    got = fused.linear(X, dev(w, gpu), fused.Epilogue(bias=dev(b, gpu), residual=dev(r, gpu)))
+    check(f"linear {n}x{k}x{m} ldx {ldx}", got.cpu().numpy(),
+          O.linear(x, w, bias=b, residual=r), bound(x, w))
+
+
+def test_bare_product_pads_narrow_m(gpu):
+    x = W.normal((300, 64), 21, 1.0)
+    w = W.normal((64, 200), 22, 0.1)
+    got = fused.linear(dev(x, gpu), dev(w, gpu))
+    assert tuple(got.shape) == (300, 200)
+    check("bare 300x64x200", got.cpu().numpy(), O.linear(x, w), bound(x, w))
+    # Odd m takes the element-wise path.
+    w = W.normal((64, 131), 23, 0.1)
+    got = fused.linear(dev(x, gpu), dev(w, gpu))
+    check("bare 300x64x131", got.cpu().numpy(), O.linear(x, w), bound(x, w))
+
+
+def test_unsupported_shapes_return_none(gpu):
+    x = dev(np.ones((4, 12), np.float32), gpu)
+    assert fused.linear(x, dev(np.ones((12, 128), np.float32), gpu)) is None        # k % 8
+    x = dev(np.ones((4, 16), np.float32), gpu)
+    b = dev(np.ones(200, np.float32), gpu)
+    assert fused.linear(x, dev(np.ones((16, 200), np.float32), gpu),
+                        fused.Epilogue(bias=b)) is None                            # m % 128
+    t = dev(np.ones((4, 3, 64), np.float32), gpu)
+    assert fused.linear(x, dev(np.ones((16, 128), np.float32), gpu),
+                        fused.Epilogue(rotary=(t, 64))) is None                    # 2w > m
+
+
+def test_norm_linear_matches_unit_norm_then_linear(gpu):
+    n, k, m = 1001, 384, 1536
+    x = W.normal((n, k), 31, 2.0)
+    x[7] = 0.0                                    # the 1e-12 floor: a zero row stays zero
+    w = W.normal((k, m), 32, 0.4)
+    b = W.normal((m,), 33, 0.1)
+    got = fused.norm_linear(dev(x, gpu), dev(w, gpu),
+                            fused.Epilogue(bias=dev(b, gpu), gelu=True)).cpu().numpy()
+    xn = O.unit_norm(x)
+    want = O.linear(xn, w, bias=b, gelu=True)
+    check("norm_linear + bias + GELU", got, want, bound(xn, w, 1.13) + 1e-6)
+
+
+@pytest.mark.parametrize("rows,dim,scaled", [(96120, 384, False), (1000, 384, True),
+                                             (33, 131, True), (4, 8, False)])
+def test_unit_norm(gpu, rows, dim, scaled):
+    x = W.normal((rows, dim), 41, 3.0)
+    x[min(2, rows - 1)] = 0.0
+    scale = (1.0 + W.normal((dim,), 42, 0.1)) * np.float32(np.sqrt(dim)) if scaled else None
+    got = fused.unit_norm(dev(x, gpu), None if scale is None else dev(scale, gpu))
+    want = O.unit_norm(x, scale)
+    err = float(np.abs(got.cpu().numpy() - want).max())
+    print(f"unit_norm {rows}x{dim}: max|diff| {err:.3e}", flush=True)
+    assert err < (2e-6 if scale is None else 5e-5)
+
+
+def _block_weights(dim, heads, hidden, normalized=True):
+    w, _ = C.layer_case() if (dim, heads, hidden) == (C.LAYER_DIM, C.LAYER_HEADS,
+                                                      C.LAYER_HIDDEN) else (None, None)
+    if w is None:
+        shapes = {
+            "attn_gamma": (dim,), "to_qkv": (3 * heads * 64, dim), "to_gates": (heads, dim),
+            "to_gates_bias": (heads,), "to_out": (dim, heads * 64), "ff_gamma": (dim,),
+            "ff_in": (hidden, dim), "ff_in_bias": (hidden,), "ff_out": (dim, hidden),
+            "ff_out_bias": (dim,), "output_gamma": (dim,)}
+        w = {"heads": heads, "freqs": W.rope_freqs()}
+        for i, (name, shape) in enumerate(sorted(shapes.items())):
+            w[name] = (1.0 + W.normal(shape, 100 + i, 0.1) if name.endswith("gamma")
+                       else W.normal(shape, 100 + i, 0.02))
+    if not normalized:
+        w = dict(w, output_gamma=None)
+    return w
+
+
+def test_block_matches_golden_layer(gpu):
+    w, x = C.layer_case()
+    block = roformer.Transformer(w, gpu)
+    table = roformer.axis_rope(w["freqs"], x.shape[1], gpu)
+    got = block(dev(x, gpu), table).cpu().numpy()
+    golden = np.load(os.path.join(GOLDEN, "layer.npz"), allow_pickle=False)["out"]
+    err = float(np.abs(got - golden).max())
+    ref = float(np.abs(O.transformer_forward(w, x, kernels=True) - golden).max())
+    print(f"block vs golden layer: max|diff| {err:.3e} (oracle f32 {ref:.1e})", flush=True)
+    assert err < 2e-3
+    xd = dev(x, gpu)
+    assert torch.equal(block(xd, table), block(xd, table))  # deterministic
+
+
+@pytest.mark.parametrize("axis", ["time", "band"])
+def test_block_attention_core_at_layer_pair_shape(gpu, axis):
+    """The dim-384 block of the layer-pair workload ([2, 60, 801, 384]) on a sample of its
+    groups: the attention-block output (packed GEMM -> gated attention) within 2e-3 of the
+    oracle, and the block output within the GEMM bound's scale."""
+    dim, heads, hidden = 384, 8, 1536
+    tokens = 801 if axis == "time" else 60
+    groups = 3
+    w = _block_weights(dim, heads, hidden, normalized=True)
+    x = W.normal((groups, tokens, dim), 4, 1.0)
+    table_np = W.axis_rope_packed(W.rope_freqs(), tokens)
+    table = dev(table_np, gpu)
+    block = roformer.Transformer(w, gpu)
+    # Attention core through the block's own packed weights and the public ops.
+    inner, columns = heads * 64, 1664
+    s = np.float32(np.sqrt(np.float32(dim))) * w["attn_gamma"]
+    wp = np.zeros((dim, columns), np.float32)
+    wp[:, :3 * inner] = (w["to_qkv"] * s[None, :]).T
+    wp[:, 3 * inner:3 * inner + heads] = (w["to_gates"] * s[None, :]).T
+    bp = np.zeros(columns, np.float32)
+    bp[3 * inner:3 * inner + heads] = w["to_gates_bias"]
+    rows = groups * tokens
+    packed = fused.norm_linear(dev(x.reshape(rows, dim), gpu), dev(wp, gpu),
+                               fused.Epilogue(bias=dev(bp, gpu), rotary=(table, inner)))
+    attended = fused.gated_attention(packed.view(groups, tokens, columns), heads).cpu().numpy()
+    xn = O.unit_norm(x.reshape(rows, dim), precision="f32")
+    packed_ref = O.linear(xn, wp, bias=bp, rope=table_np, tokens=tokens, width=inner,
+                          precision="f32").reshape(groups, tokens, columns)
+    want = O.gated_attention(packed_ref, heads)
+    err = float(np.abs(attended - want).max())
+    print(f"{axis} attention block [3, {tokens}, 384]: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
+    got = block(dev(x, gpu), table).cpu().numpy()
+    want = O.transformer_forward(w, x, kernels=True, threads=8)
+    err = float(np.abs(got - want).max())
+    print(f"{axis} block output: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
