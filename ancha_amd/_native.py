@@ -44,6 +44,9 @@ SIGNATURES = {
     "ancha_hip_block_workspace": (_sz, [_p, _sz]),
     "ancha_hip_block_forward": (_int, [_p, _p, _sz, _sz, _p, _p, _sz, _p, _p]),
     "ancha_hip_block_destroy": (None, [_p]),
+    "ancha_hip_swap_axes": (_int, [_p, _sz, _sz, _sz, _sz, _p, _p]),
+    "ancha_hip_axis_pair_workspace": (_sz, [_p, _p, _sz]),
+    "ancha_hip_axis_pair_forward": (_int, [_p, _p, _p, _sz, _sz, _sz, _p, _p, _p, _sz, _p, _p]),
     "ancha_hip_check": (_int, []),
     "ancha_hip_last_error": (ctypes.c_char_p, []),
 }

@@ -166,6 +166,38 @@ int ancha_hip_block_forward(const ancha_hip_block* b, const float* x, size_t gro
   return rc;
 }
 
+size_t ancha_hip_axis_pair_workspace(const ancha_hip_block* time, const ancha_hip_block* band,
+                                     size_t rows) {
+  if (!time || !band || time->dim != band->dim) return 0;
+  const size_t a = ancha_hip_block_workspace(time, rows), c = ancha_hip_block_workspace(band, rows);
+  return (a > c ? a : c) + 2 * rows * time->dim * sizeof(float);
+}
+
+int ancha_hip_axis_pair_forward(const ancha_hip_block* time, const ancha_hip_block* band,
+                                const float* x, size_t batch, size_t bands, size_t frames,
+                                const float* time_rope, const float* band_rope, void* workspace,
+                                size_t workspace_bytes, float* out, hipStream_t stream) {
+  if (!time || !band || time->dim != band->dim) return ANCHA_HIP_INVALID;
+  const size_t rows = batch * bands * frames, dim = time->dim;
+  if (rows == 0) return ANCHA_HIP_OK;
+  if (!x || !out || !time_rope || !band_rope || !workspace) return ANCHA_HIP_INVALID;
+  const size_t need = ancha_hip_axis_pair_workspace(time, band, rows);
+  if (workspace_bytes < need) return ANCHA_HIP_INVALID;
+  float* a = static_cast<float*>(workspace);
+  float* c = a + rows * dim;
+  void* inner = c + rows * dim;
+  const size_t inner_bytes = need - 2 * rows * dim * sizeof(float);
+  // Time pass: groups = batch * bands, sequence = frames.
+  int rc = ancha_hip_block_forward(time, x, batch * bands, frames, time_rope, inner, inner_bytes,
+                                   a, stream);
+  if (!rc) rc = ancha_hip_swap_axes(a, batch, bands, frames, dim, c, stream);
+  // Band pass: groups = batch * frames, sequence = bands.
+  if (!rc) rc = ancha_hip_block_forward(band, c, batch * frames, bands, band_rope, inner,
+                                        inner_bytes, a, stream);
+  if (!rc) rc = ancha_hip_swap_axes(a, batch, frames, bands, dim, out, stream);
+  return rc;
+}
+
 void ancha_hip_block_destroy(ancha_hip_block* b) {
   if (!b) return;
   for (float* p : {b->packed_w, b->packed_b, b->out_w, b->ff_in_w, b->ff_in_b, b->ff_out_w,

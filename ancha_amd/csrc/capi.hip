@@ -149,6 +149,30 @@ int ancha_hip_norm_linear(const float* x, size_t n, size_t k, size_t ldx, const 
                     stream, "ancha_hip_norm_linear");
 }
 
+int ancha_hip_swap_axes(const float* x, size_t batch, size_t a, size_t b, size_t dim, float* out,
+                        hipStream_t stream) {
+  if (const int s = sticky()) return s;
+  if (batch == 0 || a == 0 || b == 0 || dim == 0) return ANCHA_HIP_OK;
+  if (!x || !out) return fail(ANCHA_HIP_INVALID, "ancha_hip_swap_axes: null tensor");
+  if (x == out && a != 1 && b != 1)
+    return fail(ANCHA_HIP_INVALID, "ancha_hip_swap_axes: out must not alias x");
+  if (batch * a * b > kIntMax * size_t(4) || batch > kIntMax || a > kIntMax || b > kIntMax ||
+      dim * 4 >= (size_t(1) << 31))
+    return fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_swap_axes: too many rows");
+  if (!device_is_gfx950()) return fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_swap_axes: not a gfx950 device");
+  ancha::SwapParams p{};
+  p.x = x;
+  p.out = out;
+  p.batch = static_cast<int>(batch);
+  p.a = static_cast<int>(a);
+  p.b = static_cast<int>(b);
+  p.dim = static_cast<int>(dim);
+  const hipError_t e = ancha::launch_swap_axes(p, aligned16(x) && aligned16(out) && dim % 4 == 0,
+                                               stream);
+  if (e != hipSuccess) return hip_fail(e, "ancha_hip_swap_axes");
+  return ANCHA_HIP_OK;
+}
+
 int ancha_hip_unit_norm(const float* x, size_t rows, size_t dim, size_t ldx, const float* scale,
                         float* out, hipStream_t stream) {
   if (const int s = sticky()) return s;

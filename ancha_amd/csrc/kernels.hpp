@@ -56,4 +56,13 @@ struct NormParams {
 
 hipError_t launch_unit_norm(const NormParams& p, bool aligned, hipStream_t stream);
 
+// out [batch, b, a, dim] = x [batch, a, b, dim] with axes 1 and 2 swapped (both contiguous).
+struct SwapParams {
+  const float* x;
+  float* out;
+  int batch, a, b, dim;
+};
+
+hipError_t launch_swap_axes(const SwapParams& p, bool aligned, hipStream_t stream);
+
 }  // namespace ancha

@@ -86,3 +86,53 @@ class Transformer:
             self.close()
         except Exception:
             pass
+
+
+def swap_axes(x: torch.Tensor) -> torch.Tensor:
+    """Dense ``x.swap_dims(1, 2)`` of a [batch, a, b, dim] float32 tensor on the GPU
+    (network.rs:336-338)."""
+    if x.dim() != 4 or x.dtype != torch.float32 or not x.is_cuda:
+        raise ValueError("swap_axes takes a float32 CUDA [batch, a, b, dim] tensor")
+    x = x.contiguous()
+    batch, a, b, dim = x.shape
+    out = torch.empty((batch, b, a, dim), device=x.device, dtype=torch.float32)
+    _native.check(_native.lib().ancha_hip_swap_axes(x.data_ptr(), batch, a, b, dim,
+                                                    out.data_ptr(),
+                                                    torch.cuda.current_stream().cuda_stream))
+    return out
+
+
+class AxisPair:
+    """One time pass + band pass of the RoFormer axis loop (network.rs:333-339) over
+    x [batch, bands, frames, dim]: the time block on groups = batch*bands (sequence = frames),
+    an axis swap, the band block on groups = batch*frames (sequence = bands), a swap back."""
+
+    def __init__(self, time: Transformer, band: Transformer):
+        if time.dim != band.dim:
+            raise ValueError("time and band blocks must share dim")
+        self.time, self.band = time, band
+        self._workspace: Optional[torch.Tensor] = None
+
+    def forward(self, x: torch.Tensor, time_rope: torch.Tensor,
+                band_rope: torch.Tensor) -> torch.Tensor:
+        batch, bands, frames, dim = x.shape
+        if dim != self.time.dim or tuple(time_rope.shape) != (4, frames, 64) \
+                or tuple(band_rope.shape) != (4, bands, 64):
+            raise ValueError("x / rope shapes do not match the blocks")
+        x = x.contiguous()
+        lib = _native.lib()
+        need = int(lib.ancha_hip_axis_pair_workspace(self.time._handle, self.band._handle,
+                                                     batch * bands * frames))
+        if self._workspace is None or self._workspace.numel() < need:
+            self._workspace = torch.empty(need, dtype=torch.uint8, device=x.device)
+        out = torch.empty_like(x)
+        rc = lib.ancha_hip_axis_pair_forward(
+            self.time._handle, self.band._handle, x.data_ptr(), batch, bands, frames,
+            time_rope.contiguous().data_ptr(), band_rope.contiguous().data_ptr(),
+            self._workspace.data_ptr(), self._workspace.numel(), out.data_ptr(),
+            torch.cuda.current_stream().cuda_stream)
+        if not _native.check(rc):
+            raise ValueError("axis pair rejected the shapes")
+        return out
+
+    __call__ = forward

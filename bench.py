@@ -126,12 +126,118 @@ def copy_calibration(torch, dev, elements: int, steps: int) -> int:
     return 0
 
 
+LAYER = dict(batch=2, bands=60, frames=801, dim=384, heads=8, hidden=1536)
+
+
+def layer_weights(dim, heads, hidden, seed):
+    """Random-init block weights ~N(0, 0.02) (projections, gate W and b, FF W and b), gamma = 1,
+    no output norm, in PyTorch nn.Linear layout."""
+    from ancha_amd import workload as W
+    inner = heads * 64
+    shapes = {"to_qkv": (3 * inner, dim), "to_gates": (heads, dim), "to_gates_bias": (heads,),
+              "to_out": (dim, inner), "ff_in": (hidden, dim), "ff_in_bias": (hidden,),
+              "ff_out": (dim, hidden), "ff_out_bias": (dim,)}
+    w = {name: W.normal(shape, seed + i, 0.02) for i, (name, shape) in enumerate(shapes.items())}
+    w.update(heads=heads, attn_gamma=np.ones(dim, np.float32), ff_gamma=np.ones(dim, np.float32),
+             output_gamma=None, freqs=W.rope_freqs())
+    return w
+
+
+def layer_flops(groups, tokens, dim, heads, hidden):
+    """Algorithmic FLOPs of one block pass: QKV+gate projection (3*inner+heads columns),
+    attention 4*G*H*T^2*64, output projection, feed-forward."""
+    n, inner = groups * tokens, heads * 64
+    return (2.0 * n * dim * (3 * inner + heads) + 4.0 * groups * heads * tokens ** 2 * 64
+            + 2.0 * n * inner * dim + 4.0 * n * dim * hidden)
+
+
+def run_layer(args, torch, dev) -> int:
+    """One RoFormer layer pair (time pass then band pass) on x [2, 60, 801, 384]."""
+    from ancha_amd import roformer
+    from ancha_amd import workload as W
+    c = LAYER
+    B, NB, T, D = c["batch"], c["bands"], c["frames"], c["dim"]
+    wt = layer_weights(D, c["heads"], c["hidden"], 300)
+    wb = layer_weights(D, c["heads"], c["hidden"], 400)
+    pair = roformer.AxisPair(roformer.Transformer(wt, dev), roformer.Transformer(wb, dev))
+    x = W.normal_torch((B, NB, T, D), W.SEED_X, 1.0, device=dev)
+    tt = roformer.axis_rope(wt["freqs"], T, dev)
+    tb = roformer.axis_rope(wb["freqs"], NB, dev)
+    step = lambda: pair(x, tt, tb)
+    out = step()
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        out = step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(end) / args.steps
+    flops_time = layer_flops(B * NB, T, D, c["heads"], c["hidden"])
+    flops_band = layer_flops(B * T, NB, D, c["heads"], c["hidden"])
+    flops = flops_time + flops_band
+    achieved = flops / (gpu_ms * 1e-3) / 1e12
+    log(f"layer pair: {gpu_ms:.3f} ms/step, {achieved:.1f} TFLOP/s")
+    result = {
+        "metric": "RoFormer layer pair TFLOP/s (% MFMA peak)",
+        "value": round(flops * args.steps / wall / 1e12, 3),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: x ~ N(0,1), weights ~ N(0,0.02), gamma = 1 (seeded)",
+        "config": {"workload": "RoFormer layer pair: time pass on [120, 801, 384] then band "
+                               "pass on [1602, 60, 384]", "dim": D, "heads": c["heads"],
+                   "head_dim": 64, "ff_hidden": c["hidden"], "io": "fp32",
+                   "mfma_operands": "fp16", "accumulate": "fp32",
+                   "gflop_per_step": round(flops / 1e9, 2), "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
+                     "traffic": None, "scope": "whole layer pair (all kernels)"},
+    }
+    if not args.no_cpu_baseline:
+        log("timing the restated reference CPU path (Burn-path block) on sampled groups")
+        result["cpu_baseline"] = layer_cpu_baseline(wt, wb, x, out)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def layer_cpu_baseline(wt, wb, x, gpu_out, budget_s: float = 12.0) -> dict:
+    """The oracle's Burn-path block (separate projections, host RoPE tables, materialized score
+    tiles, groups over all host threads) on a sample of time-pass groups, timed; the rate
+    (TFLOP/s of that pass's algorithmic FLOPs) stands for the layer pair."""
+    import oracle as O
+    c = LAYER
+    threads = cpu_threads()
+    xs = x.view(-1, c["frames"], c["dim"])
+    groups = max(1, min(threads, xs.shape[0]))
+    sample = xs[:groups].cpu().numpy()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.transformer_forward(wt, sample, kernels=False, threads=threads)
+        times.append(time.perf_counter() - t0)
+        if sum(times) > budget_s:
+            break
+    t = statistics.median(times)
+    flops = layer_flops(groups, c["frames"], c["dim"], c["heads"], c["hidden"])
+    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": (f"time-pass block on {groups} of {xs.shape[0]} groups x 801 frames "
+                       f"(Burn-path restatement, groups over {threads} threads), median of "
+                       f"{len(times)} ({t:.2f} s)")}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["time", "band"], default="time")
+    ap.add_argument("--workload", choices=["time", "band", "layer"], default="time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain device copy of the workload's I/O size instead; its "
@@ -153,6 +259,8 @@ def main() -> int:
               file=sys.stderr)
         return 2
     dev = torch.device("cuda:0")
+    if args.workload == "layer":
+        return run_layer(args, torch, dev)
     shape = W.TIME_SHAPE if args.workload == "time" else W.BAND_SHAPE
     G, T, H, D = shape
     log(f"generating q, k, v {shape} on the GPU")

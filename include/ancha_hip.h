@@ -138,6 +138,28 @@ int ancha_hip_block_forward(const ancha_hip_block *block, const float *x, size_t
 
 void ancha_hip_block_destroy(ancha_hip_block *block);
 
+/* out [batch, b, a, dim] = x [batch, a, b, dim] with axes 1 and 2 swapped (contiguous; out
+ * must not alias x). Replaces the dense `swap_dims` copies between the time and band passes
+ * (network.rs:336-338; `dense` roformer.rs:57-70). */
+int ancha_hip_swap_axes(const float *x, size_t batch, size_t a, size_t b, size_t dim, float *out,
+                        hipStream_t stream);
+
+/* Device bytes of the workspace ancha_hip_axis_pair_forward needs for
+ * rows = batch*bands*frames. */
+size_t ancha_hip_axis_pair_workspace(const ancha_hip_block *time, const ancha_hip_block *band,
+                                     size_t rows);
+
+/* One time pass + band pass of the RoFormer axis loop: x, out [batch, bands, frames, dim]
+ * contiguous (out may alias x); the time block runs on groups = batch*bands with sequence
+ * frames, the band block on groups = batch*frames with sequence bands (after an axis swap),
+ * and the result is swapped back. time_rope [4, frames, 64], band_rope [4, bands, 64].
+ * Allocates nothing. Replaces one iteration of the axis loop of the RoFormer networks
+ * (network.rs:333-339). */
+int ancha_hip_axis_pair_forward(const ancha_hip_block *time, const ancha_hip_block *band,
+                                const float *x, size_t batch, size_t bands, size_t frames,
+                                const float *time_rope, const float *band_rope, void *workspace,
+                                size_t workspace_bytes, float *out, hipStream_t stream);
+
 /* Sticky device-failure check: 0, or the first HIP error (< 0) any call has met.
  * Replaces `device::check()` (src/device.rs:30-41) for this path. */
 int ancha_hip_check(void);

@@ -159,6 +159,48 @@ static float *transposed(const float *w, size_t out, size_t in) {
   return t;
 }
 
+/* anc_linear_f32 with its rows split over `threads` pthreads (the reference's Burn GEMMs run
+ * multi-threaded); slices start at multiples of `tokens` so the rotary token index r % tokens is
+ * unchanged. Every row's arithmetic is the same as in one call. */
+typedef struct {
+  const float *x, *w, *bias, *rope, *residual;
+  float *out;
+  size_t n, k, ldx, m, tokens, width;
+  int gelu;
+} lin_job;
+
+static void *lin_worker(void *arg) {
+  lin_job *j = (lin_job *)arg;
+  anc_linear_f32(j->x, j->n, j->k, j->ldx, j->w, j->m, j->bias, j->gelu, j->rope, j->tokens,
+                 j->width, j->residual, j->out);
+  return NULL;
+}
+
+static void par_linear(size_t threads, const float *x, size_t n, size_t k, size_t ldx,
+                       const float *w, size_t m, const float *bias, int gelu, const float *rope,
+                       size_t tokens, size_t width, const float *residual, float *out) {
+  size_t unit = rope ? tokens : 1;
+  size_t units = (n + unit - 1) / unit;
+  size_t parts = threads < 1 ? 1 : threads;
+  if (parts > units) parts = units;
+  if (parts <= 1) {
+    anc_linear_f32(x, n, k, ldx, w, m, bias, gelu, rope, tokens, width, residual, out);
+    return;
+  }
+  size_t per = (units + parts - 1) / parts * unit;
+  lin_job jobs[256];
+  pthread_t tids[256];
+  size_t nj = 0;
+  for (size_t r0 = 0; r0 < n && nj < 256; r0 += per, nj++) {
+    size_t rows = n - r0 < per ? n - r0 : per;
+    lin_job j = {x + r0 * ldx, w, bias, rope, residual ? residual + r0 * m : NULL, out + r0 * m,
+                 rows, k, ldx, m, tokens, width, gelu};
+    jobs[nj] = j;
+  }
+  for (size_t i = 0; i < nj; i++) pthread_create(&tids[i], NULL, lin_worker, &jobs[i]);
+  for (size_t i = 0; i < nj; i++) pthread_join(tids[i], NULL);
+}
+
 static float *source_scale(const float *gamma, size_t dim) {
   float *s = (float *)malloc(sizeof(float) * dim);
   float root = sqrtf((float)dim);
@@ -206,7 +248,7 @@ int anc_transformer_forward(const anc_block_weights *w, const float *x, size_t g
     }
     memcpy(bp + 3 * inner, bg, sizeof(float) * heads);
     float *packed = malloc(sizeof(float) * rows * columns);
-    anc_linear_f32(xn, rows, dim, dim, wp, columns, bp, 0, table, tokens, inner, NULL, packed);
+    par_linear(threads, xn, rows, dim, dim, wp, columns, bp, 0, table, tokens, inner, NULL, packed);
     rc = anc_gated_attention_f32(packed, groups, tokens, columns, heads, NULL, attended);
     free(packed);
     free(wp);
@@ -219,10 +261,10 @@ int anc_transformer_forward(const anc_block_weights *w, const float *x, size_t g
     float *ck = malloc(sizeof(float) * tokens * inner), *sk = malloc(sizeof(float) * tokens * inner);
     anc_rope_tables(w->freqs, nf, tokens, heads, 1.0f / sqrtf((float)hd), cq, sq);
     anc_rope_tables(w->freqs, nf, tokens, heads, 1.0f, ck, sk);
-    anc_linear_f32(xn, rows, dim, dim, wq, inner, NULL, 0, NULL, 1, 0, NULL, q);
-    anc_linear_f32(xn, rows, dim, dim, wk, inner, NULL, 0, NULL, 1, 0, NULL, k);
-    anc_linear_f32(xn, rows, dim, dim, wv, inner, NULL, 0, NULL, 1, 0, NULL, v);
-    anc_linear_f32(xn, rows, dim, dim, wg, heads, bg, 0, NULL, 1, 0, NULL, gt);
+    par_linear(threads, xn, rows, dim, dim, wq, inner, NULL, 0, NULL, 1, 0, NULL, q);
+    par_linear(threads, xn, rows, dim, dim, wk, inner, NULL, 0, NULL, 1, 0, NULL, k);
+    par_linear(threads, xn, rows, dim, dim, wv, inner, NULL, 0, NULL, 1, 0, NULL, v);
+    par_linear(threads, xn, rows, dim, dim, wg, heads, bg, 0, NULL, 1, 0, NULL, gt);
     /* RopeTables::apply (roformer.rs:177-186): x*cos + x[i^1]*sin */
     for (size_t r = 0; r < rows; r++) {
       size_t t = r % tokens;
@@ -255,10 +297,10 @@ int anc_transformer_forward(const anc_block_weights *w, const float *x, size_t g
     free(sk);
   }
   if (!rc) {
-    anc_linear_f32(attended, rows, inner, inner, wo, dim, NULL, 0, NULL, 1, 0, x, x1);
+    par_linear(threads, attended, rows, inner, inner, wo, dim, NULL, 0, NULL, 1, 0, x, x1);
     anc_unit_norm_f32(x1, rows, dim, NULL, xn);
-    anc_linear_f32(xn, rows, dim, dim, w1, hidden, b1, 1, NULL, 1, 0, NULL, h);
-    anc_linear_f32(h, rows, hidden, hidden, w2, dim, w->ff_out_bias, 0, NULL, 1, 0, x1, out);
+    par_linear(threads, xn, rows, dim, dim, w1, hidden, b1, 1, NULL, 1, 0, NULL, h);
+    par_linear(threads, h, rows, hidden, hidden, w2, dim, w->ff_out_bias, 0, NULL, 1, 0, x1, out);
     if (w->output_gamma) {
       float *os = source_scale(w->output_gamma, dim);
       memcpy(x1, out, sizeof(float) * rows * dim);

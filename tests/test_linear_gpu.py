@@ -193,3 +193,60 @@ def test_block_attention_core_at_layer_pair_shape(gpu, axis):
     err = float(np.abs(got - want).max())
     print(f"{axis} block output: max|diff| {err:.3e}", flush=True)
     assert err < 2e-3
+
+
+def _oracle_pair(wt, wb, x):
+    batch, bands, frames, dim = x.shape
+    y = O.transformer_forward(wt, x.reshape(batch * bands, frames, dim), kernels=True, threads=8)
+    y = y.reshape(batch, bands, frames, dim).transpose(0, 2, 1, 3).copy()
+    z = O.transformer_forward(wb, y.reshape(batch * frames, bands, dim), kernels=True, threads=8)
+    return z.reshape(batch, frames, bands, dim).transpose(0, 2, 1, 3)
+
+
+def test_swap_axes(gpu):
+    x = W.normal((2, 5, 7, 12), 51, 1.0)
+    got = roformer.swap_axes(dev(x, gpu)).cpu().numpy()
+    assert np.array_equal(got, x.transpose(0, 2, 1, 3))
+    x = W.normal((2, 60, 33, 384), 52, 1.0)
+    assert np.array_equal(roformer.swap_axes(dev(x, gpu)).cpu().numpy(), x.transpose(0, 2, 1, 3))
+
+
+def test_axis_pair_small(gpu):
+    wt, _ = C.layer_case()
+    wb = _block_weights(C.LAYER_DIM, C.LAYER_HEADS, C.LAYER_HIDDEN)
+    wb = {k: (v * np.float32(1.1) if isinstance(v, np.ndarray) and k.startswith("to_") else v)
+          for k, v in wb.items()}
+    x = W.normal((2, 5, 37, C.LAYER_DIM), 53, 1.0)
+    pair = roformer.AxisPair(roformer.Transformer(wt, gpu), roformer.Transformer(wb, gpu))
+    got = pair(dev(x, gpu), roformer.axis_rope(wt["freqs"], 37, gpu),
+               roformer.axis_rope(wb["freqs"], 5, gpu)).cpu().numpy()
+    err = float(np.abs(got - _oracle_pair(wt, wb, x)).max())
+    print(f"axis pair [2, 5, 37, 128]: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
+
+
+def test_axis_pair_layer_pair_shape(gpu):
+    """The layer-pair workload [2, 60, 801, 384]: finite, deterministic, and its band pass on
+    sampled frames equals the oracle's block applied to the GPU's own time-pass output."""
+    dim, heads, hidden, batch, bands, frames = 384, 8, 1536, 2, 60, 801
+    wt = _block_weights(dim, heads, hidden, normalized=False)
+    wb = {k: (W.normal(v.shape, 200 + i, 0.02) if isinstance(v, np.ndarray) and
+              k.startswith(("to_", "ff_in", "ff_out")) else v)
+          for i, (k, v) in enumerate(sorted(wt.items()))}
+    x = dev(W.normal((batch, bands, frames, dim), 4, 1.0), gpu)
+    tt, tb = roformer.axis_rope(W.rope_freqs(), frames, gpu), roformer.axis_rope(
+        W.rope_freqs(), bands, gpu)
+    time, band = roformer.Transformer(wt, gpu), roformer.Transformer(wb, gpu)
+    pair = roformer.AxisPair(time, band)
+    out = pair(x, tt, tb)
+    assert torch.isfinite(out).all()
+    assert torch.equal(out, pair(x, tt, tb))
+    y = roformer.swap_axes(time(x.view(batch * bands, frames, dim), tt).view(
+        batch, bands, frames, dim))                       # [batch, frames, bands, dim]
+    sample = [0, 400, 800 + frames]                       # flattened (batch, frame) groups
+    ys = y.view(batch * frames, bands, dim)[sample].cpu().numpy()
+    want = O.transformer_forward(wb, ys, kernels=True, threads=8)
+    got = out.permute(0, 2, 1, 3).reshape(batch * frames, bands, dim)[sample].cpu().numpy()
+    err = float(np.abs(got - want).max())
+    print(f"layer pair band pass on sampled frames: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
