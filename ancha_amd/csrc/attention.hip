@@ -115,13 +115,18 @@ __device__ __forceinline__ u32x4 p_fragment(f32x4 a, f32x4 b) {
 struct OutRows {
   rsrc_t out, gate;
   unsigned ld4, ldg4;
+  bool half;
 };
 
 __device__ __forceinline__ OutRows out_rows(const AttnParams& p, int g, int h) {
   const int T = p.tokens;
   OutRows o;
-  o.ld4 = (unsigned)p.heads * 256;
-  o.out = make_rsrc(p.out + ((long)g * T * p.heads + h) * 64, (unsigned)(T - 1) * o.ld4 + 256);
+  o.half = p.out_half != 0;
+  const unsigned esize = o.half ? 2 : 4;
+  o.ld4 = (unsigned)p.heads * 64 * esize;
+  o.out = make_rsrc(reinterpret_cast<unsigned char*>(p.out) +
+                        ((long)g * T * p.heads + h) * 64 * esize,
+                    (unsigned)(T - 1) * o.ld4 + 64 * esize);
   o.ldg4 = (unsigned)p.ldg * 4;
   o.gate = make_rsrc(p.gate ? p.gate + (long)g * T * p.ldg + h : p.out,
                      p.gate ? (unsigned)(T - 1) * o.ldg4 + 4 : 0);
@@ -134,6 +139,16 @@ __device__ __forceinline__ void store_output(const OutRows& o, const f32x4 (&acc
                                              int t, int grp) {
   float scale = 1.0f / l;
   if constexpr (GATED) scale = scale / (1.0f + expf(-bload1(o.gate, (unsigned)t * o.ldg4)));
+  if (o.half) {
+    const unsigned base = (unsigned)t * o.ld4 + grp * 8;
+#pragma unroll
+    for (int db = 0; db < 4; db++) {
+      const u32x2 h = {pack_h2(acc[db][0] * scale, acc[db][1] * scale),
+                       pack_h2(acc[db][2] * scale, acc[db][3] * scale)};
+      __builtin_amdgcn_raw_buffer_store_b64(h, o.out, base + db * 32, 0, 0);
+    }
+    return;
+  }
   const unsigned base = (unsigned)t * o.ld4 + grp * 16;
 #pragma unroll
   for (int db = 0; db < 4; db++)

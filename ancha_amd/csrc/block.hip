@@ -11,23 +11,28 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <cstdint>
 #include <cstring>
 #include <new>
 #include <vector>
 
 #include "../../include/ancha_hip.h"
+#include "kernels.hpp"
 
+// Weights are stored as fp16 W^T [out][in] (the PyTorch layout, folded scales applied before
+// rounding): the GEMMs round every operand to fp16 anyway, so converting once at load time
+// changes no result and halves the weight bytes each GEMM tile reads.
 struct ancha_hip_block {
   size_t dim, heads, hidden, inner, columns;
   int device;
-  float* packed_w;    // [dim, columns]
-  float* packed_b;    // [columns]
-  float* out_w;       // [inner, dim]
-  float* ff_in_w;     // [dim, hidden]
-  float* ff_in_b;     // [hidden]
-  float* ff_out_w;    // [hidden, dim]
-  float* ff_out_b;    // [dim]
-  float* out_scale;   // [dim] sqrt(dim)*output_gamma, or null
+  _Float16* packed_w;  // [columns, dim]: q | k | v | gates | zero rows
+  float* packed_b;     // [columns]
+  _Float16* out_w;     // [dim, inner]
+  _Float16* ff_in_w;   // [hidden, dim]
+  float* ff_in_b;      // [hidden]
+  _Float16* ff_out_w;  // [dim, hidden]
+  float* ff_out_b;     // [dim]
+  float* out_scale;    // [dim] sqrt(dim)*output_gamma, or null
 };
 
 namespace {
@@ -42,22 +47,50 @@ std::vector<float> source_scale(const float* gamma, size_t dim) {
   return s;
 }
 
-// W'[i][c0 + o] = W[row0 + o][i] * scale[i] for o < outs: a PyTorch [out, in] block written
-// transposed into columns [c0, c0 + outs) of a row-major [in, ld] matrix
-// (folded_linear, weights.rs:149-176).
-void fold_into(const float* w, size_t in, size_t row0, size_t outs, const float* scale,
-               float* dst, size_t ld, size_t c0) {
+// dst[(r0 + o)][i] = fp16(W[row0 + o][i] * scale[i]) for o < outs: rows of a PyTorch
+// [out, in] matrix with the folded input scale (folded_linear's W'[i][o] = W[o][i]*scale[i],
+// weights.rs:149-176, kept in [out][in] order), rounded to fp16 (round to nearest even).
+void fold_rows(const float* w, size_t in, size_t row0, size_t outs, const float* scale,
+               _Float16* dst, size_t r0) {
   for (size_t o = 0; o < outs; o++)
     for (size_t i = 0; i < in; i++)
-      dst[i * ld + c0 + o] = w[(row0 + o) * in + i] * (scale ? scale[i] : 1.0f);
+      dst[(r0 + o) * in + i] = static_cast<_Float16>(w[(row0 + o) * in + i] * (scale ? scale[i] : 1.0f));
 }
 
-int upload(const std::vector<float>& host, float** dev) {
+template <typename T>
+int upload(const std::vector<T>& host, T** dev) {
   *dev = nullptr;
   if (host.empty()) return 0;
-  hipError_t e = hipMalloc(reinterpret_cast<void**>(dev), host.size() * sizeof(float));
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(dev), host.size() * sizeof(T));
   if (e == hipSuccess)
-    e = hipMemcpy(*dev, host.data(), host.size() * sizeof(float), hipMemcpyHostToDevice);
+    e = hipMemcpy(*dev, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice);
+  return e == hipSuccess ? 0 : -static_cast<int>(e);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// One block GEMM through the fp16-weight kernel.
+int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, size_t m,
+         const float* bias, bool gelu, const float* rope, size_t tokens, size_t width,
+         const float* residual, void* out, bool out_half, bool norm, hipStream_t stream) {
+  ancha::Gemm16Params p{};
+  p.x = x;
+  p.wt = wt;
+  p.bias = bias;
+  p.rope = rope;
+  p.residual = residual;
+  p.out = out;
+  p.ldx = static_cast<long>(k);
+  p.n = static_cast<int>(n);
+  p.k = static_cast<int>(k);
+  p.m = static_cast<int>(m);
+  p.tokens = rope ? static_cast<int>(tokens) : 1;
+  p.width = rope ? static_cast<int>(width) : 0;
+  p.gelu = gelu;
+  p.norm = norm;
+  p.x_half = x_half;
+  p.out_half = out_half;
+  const hipError_t e = ancha::launch_gemm16(p, stream);
   return e == hipSuccess ? 0 : -static_cast<int>(e);
 }
 
@@ -85,18 +118,22 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
       !ancha_hip_linear_supported(dim, hidden) || !ancha_hip_linear_supported(hidden, dim))
     return ANCHA_HIP_UNSUPPORTED;
 
+  if (!ancha_hip_available()) return ANCHA_HIP_UNSUPPORTED;
+  if (dim * 4 * 128 >= (size_t(1) << 31) || hidden * 4 * 128 >= (size_t(1) << 31) ||
+      columns * 4 * 128 >= (size_t(1) << 31))
+    return ANCHA_HIP_UNSUPPORTED;
+
   const std::vector<float> norm = source_scale(attn_gamma, dim);
   const std::vector<float> ffs = source_scale(ff_gamma, dim);
-  std::vector<float> pw(dim * columns, 0.0f), pb(columns, 0.0f);
-  fold_into(to_qkv, dim, 0, inner, norm.data(), pw.data(), columns, 0);
-  fold_into(to_qkv, dim, inner, inner, norm.data(), pw.data(), columns, inner);
-  fold_into(to_qkv, dim, 2 * inner, inner, norm.data(), pw.data(), columns, 2 * inner);
-  fold_into(to_gates, dim, 0, heads, norm.data(), pw.data(), columns, 3 * inner);
+  std::vector<_Float16> pw(columns * dim, static_cast<_Float16>(0.0f));
+  std::vector<float> pb(columns, 0.0f);
+  fold_rows(to_qkv, dim, 0, 3 * inner, norm.data(), pw.data(), 0);
+  fold_rows(to_gates, dim, 0, heads, norm.data(), pw.data(), 3 * inner);
   for (size_t h = 0; h < heads; h++) pb[3 * inner + h] = to_gates_bias[h];
-  std::vector<float> ow(inner * dim), w1(dim * hidden), w2(hidden * dim);
-  fold_into(to_out, inner, 0, dim, nullptr, ow.data(), dim, 0);
-  fold_into(ff_in, dim, 0, hidden, ffs.data(), w1.data(), hidden, 0);
-  fold_into(ff_out, hidden, 0, dim, nullptr, w2.data(), dim, 0);
+  std::vector<_Float16> ow(dim * inner), w1(hidden * dim), w2(dim * hidden);
+  fold_rows(to_out, inner, 0, dim, nullptr, ow.data(), 0);
+  fold_rows(ff_in, dim, 0, hidden, ffs.data(), w1.data(), 0);
+  fold_rows(ff_out, hidden, 0, dim, nullptr, w2.data(), 0);
   const std::vector<float> b1(ff_in_bias, ff_in_bias + hidden), b2(ff_out_bias, ff_out_bias + dim);
   std::vector<float> os;
   if (output_gamma) os = source_scale(output_gamma, dim);
@@ -126,11 +163,16 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
   return ANCHA_HIP_OK;
 }
 
+// Workspace regions: the packed projection (fp32 [rows, columns]; later the fp16 FF hidden
+// activation [rows, hidden]), the fp16 attention output [rows, inner], x + attention (fp32).
+static size_t region_packed(const ancha_hip_block* b, size_t rows) {
+  const size_t p = rows * b->columns * 4, h = rows * b->hidden * 2;
+  return round_up(p > h ? p : h, 256);
+}
+
 size_t ancha_hip_block_workspace(const ancha_hip_block* b, size_t rows) {
   if (!b) return 0;
-  // packed projection (later reused for the FF hidden activation), attention output, x + attn.
-  const size_t first = b->columns > b->hidden ? b->columns : b->hidden;
-  return rows * (round_up(first, 64) + b->inner + b->dim) * sizeof(float);
+  return region_packed(b, rows) + round_up(rows * b->inner * 2, 256) + rows * b->dim * 4;
 }
 
 int ancha_hip_block_forward(const ancha_hip_block* b, const float* x, size_t groups,
@@ -141,26 +183,48 @@ int ancha_hip_block_forward(const ancha_hip_block* b, const float* x, size_t gro
   if (rows == 0) return ANCHA_HIP_OK;
   if (!x || !out || !rope || !workspace) return ANCHA_HIP_INVALID;
   if (workspace_bytes < ancha_hip_block_workspace(b, rows)) return ANCHA_HIP_INVALID;
-  const size_t first = b->columns > b->hidden ? b->columns : b->hidden;
-  float* packed = static_cast<float*>(workspace);       // [rows, columns], then [rows, hidden]
-  float* attended = packed + rows * round_up(first, 64);  // [rows, inner]
-  float* x1 = attended + rows * b->inner;                // [rows, dim]
+  if (!aligned16(x) || !aligned16(out) || !aligned16(rope) || !aligned16(workspace))
+    return ANCHA_HIP_INVALID;
+  if (rows > 0x7fffffff || rows * b->columns * 4 >= (size_t(1) << 40))
+    return ANCHA_HIP_UNSUPPORTED;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev != b->device) return ANCHA_HIP_INVALID;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  float* packed = reinterpret_cast<float*>(ws);                      // [rows, columns] fp32
+  _Float16* hidden = reinterpret_cast<_Float16*>(ws);                // [rows, hidden] fp16
+  _Float16* attended = reinterpret_cast<_Float16*>(ws + region_packed(b, rows));
+  float* x1 = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(attended) +
+                                       round_up(rows * b->inner * 2, 256));
   const size_t dim = b->dim, inner = b->inner;
-  int rc = ancha_hip_norm_linear(x, rows, dim, dim, b->packed_w, b->columns, b->packed_b, 0, rope,
-                                 tokens, inner, nullptr, packed, stream);
+  // packed = unit_norm(x) . [Wq|Wk|Wv|Wg|0] + [0|0|0|bg|0], RoPE on the q / k columns.
+  int rc = gemm(x, false, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
+                inner, nullptr, packed, false, true, stream);
   if (rc) return rc;
-  rc = ancha_hip_gated_attention(packed, groups, tokens, b->columns, b->heads, nullptr, attended,
-                                 stream);
+  // attended = softmax(q k^T) v * sigmoid(gate), stored fp16.
+  ancha::AttnParams ap{};
+  ap.q = packed;
+  ap.k = packed + inner;
+  ap.v = packed + 2 * inner;
+  ap.gate = packed + 3 * inner;
+  ap.out = reinterpret_cast<float*>(attended);
+  ap.ldq = ap.ldk = ap.ldv = ap.ldg = static_cast<long>(b->columns);
+  ap.groups = static_cast<int>(groups);
+  ap.tokens = static_cast<int>(tokens);
+  ap.heads = static_cast<int>(b->heads);
+  ap.out_half = 1;
+  hipError_t e = ancha::launch_attention(ap, true, stream);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  // x1 = x + attended . W_out
+  rc = gemm(attended, true, rows, inner, b->out_w, dim, nullptr, false, nullptr, 0, 0, x, x1,
+            false, false, stream);
   if (rc) return rc;
-  rc = ancha_hip_linear(attended, rows, inner, inner, b->out_w, dim, nullptr, 0, nullptr, 0, 0, x,
-                        x1, stream);
+  // hidden = GELU(unit_norm(x1) . W1' + b1), stored fp16.
+  rc = gemm(x1, false, rows, dim, b->ff_in_w, b->hidden, b->ff_in_b, true, nullptr, 0, 0, nullptr,
+            hidden, true, true, stream);
   if (rc) return rc;
-  float* hidden = packed;
-  rc = ancha_hip_norm_linear(x1, rows, dim, dim, b->ff_in_w, b->hidden, b->ff_in_b, 1, nullptr, 0,
-                             0, nullptr, hidden, stream);
-  if (rc) return rc;
-  rc = ancha_hip_linear(hidden, rows, b->hidden, b->hidden, b->ff_out_w, dim, b->ff_out_b, 0,
-                        nullptr, 0, 0, x1, out, stream);
+  // out = x1 + hidden . W2 + b2
+  rc = gemm(hidden, true, rows, b->hidden, b->ff_out_w, dim, b->ff_out_b, false, nullptr, 0, 0,
+            x1, out, false, false, stream);
   if (rc) return rc;
   if (b->out_scale) rc = ancha_hip_unit_norm(out, rows, dim, dim, b->out_scale, out, stream);
   return rc;
@@ -200,8 +264,10 @@ int ancha_hip_axis_pair_forward(const ancha_hip_block* time, const ancha_hip_blo
 
 void ancha_hip_block_destroy(ancha_hip_block* b) {
   if (!b) return;
-  for (float* p : {b->packed_w, b->packed_b, b->out_w, b->ff_in_w, b->ff_in_b, b->ff_out_w,
-                   b->ff_out_b, b->out_scale})
+  for (void* p : {static_cast<void*>(b->packed_w), static_cast<void*>(b->packed_b),
+                  static_cast<void*>(b->out_w), static_cast<void*>(b->ff_in_w),
+                  static_cast<void*>(b->ff_in_b), static_cast<void*>(b->ff_out_w),
+                  static_cast<void*>(b->ff_out_b), static_cast<void*>(b->out_scale)})
     if (p) (void)hipFree(p);
   delete b;
 }

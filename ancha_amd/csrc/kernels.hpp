@@ -13,9 +13,10 @@ struct AttnParams {
   const float* v;
   const float* gate;  // per-head gate logits (head h at +h), or null
   const float* rope;  // packed [4, tokens, 64] table, or null (q/k already rotated, q scaled)
-  float* out;         // [groups, tokens, heads, 64] contiguous
+  float* out;         // [groups, tokens, heads, 64] contiguous (fp16 values if out_half)
   long ldq, ldk, ldv, ldg;
   int groups, tokens, heads;
+  int out_half;       // store the output as fp16 (the block's internal activation)
 };
 
 // `aligned`: every float4 access is 16-byte aligned (base pointers and row strides).
@@ -55,6 +56,25 @@ struct NormParams {
 };
 
 hipError_t launch_unit_norm(const NormParams& p, bool aligned, hipStream_t stream);
+
+// The block's projection GEMM on load-time fp16 weights: out = epilogue(x . W) with W^T fp16
+// [m][k] (k contiguous, the PyTorch [out, in] layout), x fp32 or fp16 (x_half) [n][k] with row
+// stride ldx, out fp32 or fp16 (out_half) [n][m] contiguous; bias, rope, residual (fp32) and
+// the row norm as in LinearParams. Requires m % 128 == 0, k % 8 == 0, 16-byte aligned rows.
+struct Gemm16Params {
+  const void* x;
+  const _Float16* wt;
+  const float* bias;
+  const float* rope;
+  const float* residual;
+  void* out;
+  long ldx;
+  int n, k, m;
+  int tokens, width;
+  int gelu, norm, x_half, out_half;
+};
+
+hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream);
 
 // out [batch, b, a, dim] = x [batch, a, b, dim] with axes 1 and 2 swapped (both contiguous).
 struct SwapParams {
