@@ -18,9 +18,9 @@
 //    on the way), double buffered, the next tile's loads in flight while the current one is
 //    multiplied. The online softmax rescales lazily: the running maximum only moves when a
 //    tile exceeds it by more than kTau, so most tiles skip the O / l rescale.
-//  * attention_band_kernel: T <= 64 (the band axis, 60-62 bands, huge batch). One wave owns one
-//    whole (group, head) problem: K and Q fragments come straight from global memory into
-//    registers, V goes through a wave-private LDS transpose, softmax is exact (one key tile).
+//  * attention_band_kernel: T <= 64 (the band axis, 60-62 bands, huge batch). One 4-wave
+//    workgroup per (group, head) problem stages q, k (rotated) and v^T through LDS with
+//    coalesced row loads, then each wave takes 16 queries; softmax is exact (one key tile).
 #include <type_traits>
 
 #include "buffer.hpp"
@@ -45,56 +45,8 @@ constexpr int kWaitVmem = 0x0F70;
 // fp16 1.0 in both halves of a dword: the A operand of the row-sum MFMA.
 constexpr unsigned kOnesH2 = 0x3C003C00u;
 
-// 8-byte chunk swizzle of a transposed V^T row `d` (64 keys = 16 chunks of 4 fp16): keeps both
-// the 4x4-block transposing writes and the MFMA operand reads free of LDS bank conflicts.
-__device__ __forceinline__ int vt_swizzle(int d) { return ((d >> 2) ^ (d << 2)) & 15; }
-
 // Byte offset of 16-byte chunk c (8 fp16 channels) of K row r in a [64][64] fp16 tile.
 __device__ __forceinline__ int k_offset(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
-
-// Channels [d, d+8) of row t (0 past the end), rotated with the table rows (cos at table ct,
-// signed sin at ct + 1) when ROPE, scaled, packed to fp16.
-template <bool ROPE, bool ALIGNED>
-__device__ __forceinline__ u32x4 load_fragment(rsrc_t x, unsigned ld4, rsrc_t table, int T, int t,
-                                               int d, int ct, float scale) {
-  const unsigned off = (unsigned)t * ld4 + d * 4;
-  float4 a = bload4<ALIGNED>(x, off), b = bload4<ALIGNED>(x, off + 16);
-  if constexpr (ROPE) {
-    // cos values at even channels of table ct, +sin values at odd channels of table ct + 1.
-    const unsigned c = ((unsigned)(ct * T + t) * 64 + d) * 4, s = c + (unsigned)T * 256 + 4;
-    a = rotate_pairs(a, bload1(table, c), bload1(table, c + 8), bload1(table, s),
-                     bload1(table, s + 8));
-    b = rotate_pairs(b, bload1(table, c + 16), bload1(table, c + 24), bload1(table, s + 16),
-                     bload1(table, s + 24));
-  }
-  a = scale4(a, scale);
-  b = scale4(b, scale);
-  return u32x4{pack_h2(a.x, a.y), pack_h2(a.z, a.w), pack_h2(b.x, b.y), pack_h2(b.z, b.w)};
-}
-
-// Writes a 4-key x 4-channel block (rows r = 0..3 of `vr` are keys 4*kq+r, channels 4*dq..+3)
-// transposed into the V^T tile: row 4*dq+j gets keys 4*kq..4*kq+3 as one 8-byte chunk.
-__device__ __forceinline__ void store_vt_block(unsigned char* vt, const float4 (&vr)[4], int kq,
-                                               int dq) {
-#pragma unroll
-  for (int j = 0; j < 4; j++) {
-    const int d = dq * 4 + j;
-    const u32x2 w = {pack_h2(comp(vr[0], j), comp(vr[1], j)),
-                     pack_h2(comp(vr[2], j), comp(vr[3], j))};
-    *reinterpret_cast<u32x2*>(vt + d * 128 + ((kq ^ vt_swizzle(d)) << 3)) = w;
-  }
-}
-
-// A operand of O^T = V^T.P^T for channel block db and 32-key step ks: lane holds channel
-// db*16 + col and keys ks*32 + {grp*4 + i, 16 + grp*4 + i}, i = 0..3.
-__device__ __forceinline__ u32x4 vt_fragment(const unsigned char* vt, int db, int ks, int col,
-                                             int grp) {
-  const int d = db * 16 + col, sw = vt_swizzle(d);
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(vt + d * 128 + (((ks * 8 + grp) ^ sw) << 3));
-  const u32x2 hi =
-      *reinterpret_cast<const u32x2*>(vt + d * 128 + (((ks * 8 + 4 + grp) ^ sw) << 3));
-  return u32x4{lo.x, lo.y, hi.x, hi.y};
-}
 
 // Chunked V^T tile (time kernel): row d holds the 64 keys of channel d, and the 16-byte chunk
 // ks*4 + grp holds keys ks*32 + {grp*4 + i, 16 + grp*4 + i} (i = 0..3) in that order, so one
@@ -469,122 +421,114 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
 }
 
 // ------------------------------------------------------------------------------------------
-// Short sequences (T <= 64): one wave per (group, head), 4 problems per workgroup.
+// Short sequences (T <= 64): one workgroup (4 waves) per (group, head) problem. The whole
+// workgroup stages q, k (rotated, fp16) and v^T (fp16) through LDS with coalesced 16-byte row
+// loads, all issued at once; then wave w computes queries 16w .. 16w+15 against all keys with
+// an exact softmax. Small workgroups with few registers keep many problems' loads in flight
+// per CU, which is what this HBM-bound shape needs.
 // ------------------------------------------------------------------------------------------
 template <bool GATED, bool ROPE, bool ALIGNED>
 __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int problems) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds_v[4][64 * 128];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ __attribute__((aligned(16))) unsigned char lds_q[64 * 128];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_k[64 * 128];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_v[64 * 128];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int prob = blockIdx.x * 4 + wave;
-  const bool active = prob < problems;
-  const int pr = active ? prob : 0;
-  const int h = pr % p.heads, g = pr / p.heads;
+  const int prob = blockIdx.x;
+  const int h = prob % p.heads, g = prob / p.heads;
   const int T = p.tokens;
   const unsigned ldq4 = (unsigned)p.ldq * 4, ldk4 = (unsigned)p.ldk * 4,
                  ldv4 = (unsigned)p.ldv * 4;
   const rsrc_t qr = make_rsrc(p.q + (long)g * T * p.ldq + h * 64, (unsigned)(T - 1) * ldq4 + 256);
   const rsrc_t kr = make_rsrc(p.k + (long)g * T * p.ldk + h * 64, (unsigned)(T - 1) * ldk4 + 256);
   const rsrc_t vr = make_rsrc(p.v + (long)g * T * p.ldv + h * 64, (unsigned)(T - 1) * ldv4 + 256);
-  const rsrc_t tr = make_rsrc(ROPE ? p.rope : p.q, ROPE ? (unsigned)T * 1024 : 0);
-  unsigned char* vt = lds_v[wave];
 
-  if (active) {
-    // V^T through LDS: lane owns the 4x4 blocks (keys 4*kq..+3, channels 4*col..+3),
-    // kq = grp + 4*it.
+  // Staging: q / k rows srow + 16*it at channels 4*sc; v key pairs (2*(srow + 16*it), +1),
+  // it < 2. Rows at or past T read as 0.
+  const int srow = tid >> 4, sc = tid & 15;
+  float4 xq[4], xk[4], xv[4];
+#pragma unroll
+  for (int it = 0; it < 4; it++) {
+    const unsigned r = (unsigned)(srow + 16 * it);
+    xq[it] = bload4<ALIGNED>(qr, r * ldq4 + sc * 16);
+    xk[it] = bload4<ALIGNED>(kr, r * ldk4 + sc * 16);
+  }
+#pragma unroll
+  for (int it = 0; it < 2; it++)
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+      xv[it * 2 + r] = bload4<ALIGNED>(vr, (unsigned)(2 * (srow + 16 * it) + r) * ldv4 + sc * 16);
+  if constexpr (ROPE) {
+    const rsrc_t tr = make_rsrc(p.rope, (unsigned)T * 1024);
 #pragma unroll
     for (int it = 0; it < 4; it++) {
-      const int kq = grp + 4 * it;
-      float4 v4[4];
-#pragma unroll
-      for (int r = 0; r < 4; r++)
-        v4[r] = bload4<ALIGNED>(vr, (unsigned)(kq * 4 + r) * ldv4 + col * 16);
-      store_vt_block(vt, v4, kq, col);
+      const unsigned o = (unsigned)(srow + 16 * it) * 256 + sc * 16, plane = (unsigned)T * 256;
+      xq[it] = rotate4(xq[it], bload4<ALIGNED>(tr, o), bload4<ALIGNED>(tr, o + plane));
+      xk[it] = rotate4(xk[it], bload4<ALIGNED>(tr, o + 2 * plane), bload4<ALIGNED>(tr, o + 3 * plane));
     }
   }
+#pragma unroll
+  for (int it = 0; it < 4; it++) {
+    const int r = srow + 16 * it;
+    const float4 q = scale4(xq[it], kLog2e), k = xk[it];
+    const int off = k_offset(r, sc >> 1) + ((sc & 1) << 3);
+    *reinterpret_cast<u32x2*>(lds_q + off) = u32x2{pack_h2(q.x, q.y), pack_h2(q.z, q.w)};
+    *reinterpret_cast<u32x2*>(lds_k + off) = u32x2{pack_h2(k.x, k.y), pack_h2(k.z, k.w)};
+  }
+#pragma unroll
+  for (int it = 0; it < 2; it++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+      *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+          pack_h2(comp(xv[it * 2], j), comp(xv[it * 2 + 1], j));
   __syncthreads();
-  if (!active) return;
 
-  // A operand of S^T = K.Q^T: key kb*16 + col, channels ds*32 + grp*8 .. +7 (rotated).
-  u32x4 kf[4][2];
+  const int q0 = wave * 16;
+  if (q0 >= T) return;
+  const int kq_base[2] = {k_offset(col, grp), k_offset(col, 4 + grp)};
+  const int v_base[2] = {col * 128 + ((grp ^ (col & 7)) << 4),
+                         col * 128 + (((4 + grp) ^ (col & 7)) << 4)};
+  const u32x4 qf[2] = {*reinterpret_cast<const u32x4*>(lds_q + kq_base[0] + wave * 2048),
+                       *reinterpret_cast<const u32x4*>(lds_q + kq_base[1] + wave * 2048)};
+  f32x4 s[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++) {
+    s[kb] = zero4();
+#pragma unroll
+    for (int ds = 0; ds < 2; ds++)
+      s[kb] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_k + kq_base[ds] + kb * 2048),
+                           qf[ds], s[kb]);
+  }
+  if (T < 64) {
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        if (kb * 16 + grp * 4 + r >= T) s[kb][r] = kMasked;
+  }
+  float mx = kMasked;
 #pragma unroll
   for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-    for (int ds = 0; ds < 2; ds++)
-      kf[kb][ds] = load_fragment<ROPE, ALIGNED>(kr, ldk4, tr, T, kb * 16 + col, ds * 32 + grp * 8,
-                                                2, 1.0f);
-  const OutRows out = out_rows(p, g, h);
+    for (int r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][r]);
+  mx = max_over_rows(mx);
+#pragma unroll
+  for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) s[kb][r] = fast_exp2(s[kb][r] - mx);
+  const u32x4 pf[2] = {p_fragment(s[0], s[1]), p_fragment(s[2], s[3])};
   const u32x4 ones = {kOnesH2, kOnesH2, kOnesH2, kOnesH2};
-
+  f32x4 o[4] = {zero4(), zero4(), zero4(), zero4()}, lsum = zero4();
 #pragma unroll
-  for (int qp = 0; qp < 2; qp++) {
-    u32x4 qf[2][2];
+  for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
-    for (int qb = 0; qb < 2; qb++)
-#pragma unroll
-      for (int ds = 0; ds < 2; ds++)
-        qf[qb][ds] = load_fragment<ROPE, ALIGNED>(qr, ldq4, tr, T, (qp * 2 + qb) * 16 + col,
-                                                  ds * 32 + grp * 8, 0, kLog2e);
-    f32x4 s[4][2];
-#pragma unroll
-    for (int kb = 0; kb < 4; kb++) {
-      s[kb][0] = zero4();
-      s[kb][1] = zero4();
-#pragma unroll
-      for (int ds = 0; ds < 2; ds++) {
-        s[kb][0] = mfma16x16x32(kf[kb][ds], qf[0][ds], s[kb][0]);
-        s[kb][1] = mfma16x16x32(kf[kb][ds], qf[1][ds], s[kb][1]);
-      }
-    }
-    if (T < 64) {
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-        for (int r = 0; r < 4; r++)
-          if (kb * 16 + grp * 4 + r >= T) {
-            s[kb][0][r] = kMasked;
-            s[kb][1][r] = kMasked;
-          }
-    }
-    u32x4 pf[2][2];
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-      float mx = kMasked;
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][qb][r]);
-      mx = max_over_rows(mx);
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) s[kb][qb][r] = fast_exp2(s[kb][qb][r] - mx);
-      pf[0][qb] = p_fragment(s[0][qb], s[1][qb]);
-      pf[1][qb] = p_fragment(s[2][qb], s[3][qb]);
-    }
-    f32x4 o[4][2], lsum[2] = {zero4(), zero4()};
-#pragma unroll
-    for (int db = 0; db < 4; db++) {
-      o[db][0] = zero4();
-      o[db][1] = zero4();
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-      for (int db = 0; db < 4; db++) {
-        const u32x4 vf = vt_fragment(vt, db, ks, col, grp);
-        o[db][0] = mfma16x16x32(vf, pf[ks][0], o[db][0]);
-        o[db][1] = mfma16x16x32(vf, pf[ks][1], o[db][1]);
-      }
-      lsum[0] = mfma16x16x32(ones, pf[ks][0], lsum[0]);
-      lsum[1] = mfma16x16x32(ones, pf[ks][1], lsum[1]);
-    }
-#pragma unroll
-    for (int qb = 0; qb < 2; qb++) {
-      const f32x4 oq[4] = {o[0][qb], o[1][qb], o[2][qb], o[3][qb]};
-      store_output<GATED, ALIGNED>(out, oq, lsum[qb][0], (qp * 2 + qb) * 16 + col, grp);
-    }
+    for (int db = 0; db < 4; db++)
+      o[db] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_v + v_base[ks] + db * 2048),
+                           pf[ks], o[db]);
+    lsum = mfma16x16x32(ones, pf[ks], lsum);
   }
+  store_output<GATED, ALIGNED>(out_rows(p, g, h), o, lsum[0], q0 + col, grp);
 }
 
 template <bool GATED, bool ROPE, bool ALIGNED>
@@ -592,8 +536,8 @@ static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
   const int T = p.tokens;
   if (T <= 64) {
     const int problems = p.groups * p.heads;
-    hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED>), dim3((problems + 3) / 4),
-                       dim3(256), 0, stream, p, problems);
+    hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED>), dim3(problems), dim3(256), 0,
+                       stream, p, problems);
   } else {
     const int qblocks = (T + kTimeQueries - 1) / kTimeQueries;
     const int total = p.groups * p.heads * qblocks;
