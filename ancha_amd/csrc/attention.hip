@@ -323,9 +323,13 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
       }
     };
     // Column maximum of a unit's scores and the rescale it may trigger (per query column,
-    // under the exec mask, in place).
+    // under the exec mask, in place). Scores are s - m, so a rescale is needed only where some
+    // lane's own maximum exceeds kTau: when no lane of the wave does (the common case once m
+    // has settled) the cross-lane maximum is skipped with one wave-uniform branch.
     auto settle = [&](int qb, f32x4 (&acc)[2]) {
-      const float cm = column_max(lane_max(acc));
+      const float lm = lane_max(acc);
+      if (!__builtin_amdgcn_uicmp(lm > kTau, 0, 33)) return;  // 33: "ne" -> lane mask
+      const float cm = column_max(lm);
       if (cm > kTau) {
         const float alpha = fast_exp2(-cm);
         m[qb] += cm;
