@@ -302,101 +302,101 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
     }
   }
 
-  // One 64-key tile: 8 work units u = (half u/4, query block u%4). Unit u exponentiates its
-  // scores while the MFMAs of unit u+1's scores run, then issues its PV (and row-sum) MFMAs
-  // while the VALU takes unit u+1's maxima. MASK: keys at or past T exist in this tile.
+  // One 64-key tile: 4 work units u = query block u, each over all 64 keys. Unit u
+  // exponentiates its scores while the MFMAs of unit u+1's scores run, then issues its PV
+  // MFMAs while the VALU takes unit u+1's maxima. MASK: keys at or past T exist in this tile.
   auto tile = [&](auto mask_tag, int j) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int buf = j & 1, key0 = j * 64;
     const unsigned char* K = lds_k[buf];
     const unsigned char* V = lds_v[buf];
     u32x4 kf[2][2][2], vf[2][4];  // [half][kb2][ds], [half][db]
-    u32x4 qf[2][2];               // Q fragments of the next two units, double buffered
-    f32x4 sa[2], sb[2];
-    auto mask_scores = [&](int half, f32x4 (&acc)[2]) {
+    u32x4 qf[2][2];               // Q fragments of the next unit, double buffered
+    f32x4 sa[4], sb[4];           // [kb]: keys kb*16 + grp*4 + r
+    auto score4 = [&](const u32x4 (&qq)[2], float init, f32x4 (&acc)[4]) {
+      const f32x4 c = {init, init, init, init};
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) acc[kb] = mfma16x16x32(kf[kb >> 1][kb & 1][0], qq[0], c);
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) acc[kb] = mfma16x16x32(kf[kb >> 1][kb & 1][1], qq[1], acc[kb]);
+    };
+    auto mask_scores = [&](f32x4 (&acc)[4]) {
       if constexpr (MASK) {
 #pragma unroll
-        for (int kb2 = 0; kb2 < 2; kb2++)
+        for (int kb = 0; kb < 4; kb++)
 #pragma unroll
           for (int r = 0; r < 4; r++)
-            if (key0 + (half * 2 + kb2) * 16 + grp * 4 + r >= T) acc[kb2][r] = kMasked;
+            if (key0 + kb * 16 + grp * 4 + r >= T) acc[kb][r] = kMasked;
       }
     };
-    // Column maximum of a unit's scores and the rescale it may trigger (per query column,
-    // under the exec mask, in place). Scores are s - m, so a rescale is needed only where some
-    // lane's own maximum exceeds kTau: when no lane of the wave does (the common case once m
-    // has settled) the cross-lane maximum is skipped with one wave-uniform branch.
-    auto settle = [&](int qb, f32x4 (&acc)[2]) {
-      const float lm = lane_max(acc);
-      if (!__builtin_amdgcn_uicmp(lm > kTau, 0, 33)) return;  // 33: "ne" -> lane mask
-      const float cm = column_max(lm);
+    auto settle = [&](int qb, f32x4 (&acc)[4]) {
+      const float lm = fmaxf(fmaxf(fmaxf(acc[0][0], acc[0][1]), fmaxf(acc[0][2], acc[0][3])),
+                             fmaxf(fmaxf(acc[1][0], acc[1][1]), fmaxf(acc[1][2], acc[1][3])));
+      const float lm2 = fmaxf(fmaxf(fmaxf(acc[2][0], acc[2][1]), fmaxf(acc[2][2], acc[2][3])),
+                              fmaxf(fmaxf(acc[3][0], acc[3][1]), fmaxf(acc[3][2], acc[3][3])));
+      const float l = fmaxf(lm, lm2);
+      if (!__builtin_amdgcn_uicmp(l > kTau, 0, 33)) return;
+      const float cm = column_max(l);
       if (cm > kTau) {
         const float alpha = fast_exp2(-cm);
         m[qb] += cm;
-        acc[0] -= cm;
-        acc[1] -= cm;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) acc[kb] -= cm;
         lsum[qb] *= alpha;
 #pragma unroll
         for (int db = 0; db < 4; db++) scale_in_place(o[db][qb], alpha);
       }
     };
 #pragma unroll
-    for (int kb2 = 0; kb2 < 2; kb2++)
+    for (int h2 = 0; h2 < 2; h2++)
 #pragma unroll
-      for (int ds = 0; ds < 2; ds++) kf[0][kb2][ds] = k_frag(K, 0, kb2, ds);
+      for (int kb2 = 0; kb2 < 2; kb2++)
+#pragma unroll
+        for (int ds = 0; ds < 2; ds++) kf[h2][kb2][ds] = k_frag(K, h2, kb2, ds);
     qf[0][0] = q_frag(0, 0);
     qf[0][1] = q_frag(0, 1);
     qf[1][0] = q_frag(1, 0);
     qf[1][1] = q_frag(1, 1);
 #pragma unroll
-    for (int db = 0; db < 4; db++) vf[0][db] = v_frag(V, 0, db);
-    score(kf[0], qf[0], -m[0], sa);
-    mask_scores(0, sa);
+    for (int h2 = 0; h2 < 2; h2++)
+#pragma unroll
+      for (int db = 0; db < 4; db++) vf[h2][db] = v_frag(V, h2, db);
+    score4(qf[0], -m[0], sa);
+    mask_scores(sa);
     settle(0, sa);
 #pragma unroll
-    for (int u = 0; u < 8; u++) {
-      const int half = u >> 2, qb = u & 3;
-      const int nhalf = (u + 1) >> 2, nqb = (u + 1) & 3;
+    for (int u = 0; u < 4; u++) {
       __builtin_amdgcn_sched_barrier(0);
-      if (u == 2) {
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; kb2++)
-#pragma unroll
-          for (int ds = 0; ds < 2; ds++) kf[1][kb2][ds] = k_frag(K, 1, kb2, ds);
+      if (u + 2 < 4) {
+        qf[u & 1][0] = q_frag(u + 2, 0);
+        qf[u & 1][1] = q_frag(u + 2, 1);
       }
-      if (u == 3) {
+      if (u + 1 < 4) score4(qf[(u + 1) & 1], -m[u + 1], sb);
 #pragma unroll
-        for (int db = 0; db < 4; db++) vf[1][db] = v_frag(V, 1, db);
-      }
-      if (u + 2 < 8) {
-        qf[u & 1][0] = q_frag((u + 2) & 3, 0);
-        qf[u & 1][1] = q_frag((u + 2) & 3, 1);
-      }
-      // Phase A: next unit's S MFMAs interleaved with this unit's exponentials.
-      if (u + 1 < 8) score(kf[nhalf], qf[(u + 1) & 1], -m[nqb], sb);
+      for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; kb2++)
+        for (int r = 0; r < 4; r++) sa[kb][r] = fast_exp2(sa[kb][r]);
+      const u32x4 pf0 = p_fragment(sa[0], sa[1]), pf1 = p_fragment(sa[2], sa[3]);
+      lsum[u] += (((sa[0][0] + sa[0][1]) + (sa[0][2] + sa[0][3])) +
+                  ((sa[1][0] + sa[1][1]) + (sa[1][2] + sa[1][3]))) +
+                 (((sa[2][0] + sa[2][1]) + (sa[2][2] + sa[2][3])) +
+                  ((sa[3][0] + sa[3][1]) + (sa[3][2] + sa[3][3])));
+      if (u + 1 < 4) {
 #pragma unroll
-        for (int r = 0; r < 4; r++) sa[kb2][r] = fast_exp2(sa[kb2][r]);
-      const u32x4 pf = p_fragment(sa[0], sa[1]);
-      // Per-lane partial row sum; the four lanes of a column are added in the epilogue.
-      lsum[qb] += ((sa[0][0] + sa[0][1]) + (sa[0][2] + sa[0][3])) +
-                  ((sa[1][0] + sa[1][1]) + (sa[1][2] + sa[1][3]));
-      if (u + 1 < 8) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
+        for (int i = 0; i < 8; i++) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
           __builtin_amdgcn_sched_group_barrier(0x400, 2, 0);  // transcendental
         }
       }
-      // Phase B: this unit's PV / row-sum MFMAs, then the next unit's maxima.
 #pragma unroll
-      for (int db = 0; db < 4; db++) o[db][qb] = mfma16x16x32(vf[half][db], pf, o[db][qb]);
-      if (u + 1 < 8) {
-        mask_scores(nhalf, sb);
-        settle(nqb, sb);
-        sa[0] = sb[0];
-        sa[1] = sb[1];
+      for (int db = 0; db < 4; db++) o[db][u] = mfma16x16x32(vf[0][db], pf0, o[db][u]);
+#pragma unroll
+      for (int db = 0; db < 4; db++) o[db][u] = mfma16x16x32(vf[1][db], pf1, o[db][u]);
+      if (u + 1 < 4) {
+        mask_scores(sb);
+        settle(u + 1, sb);
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) sa[kb] = sb[kb];
       }
     }
   };
