@@ -29,14 +29,6 @@
 
 namespace ancha {
 
-// Interleaved rotation of channels (2i, 2i+1), (2i+2, 2i+3) by pair angles with cosines
-// (c0, c1) and sines (s0, s1): the same x*cos + swap_pairs(x)*sin as the packed table encodes
-// ([c, c] cosine pairs, [-s, s] sine pairs), from only the distinct table values.
-__device__ __forceinline__ float4 rotate_pairs(float4 x, float c0, float c1, float s0, float s1) {
-  return make_float4(x.x * c0 - x.y * s0, x.y * c0 + x.x * s0, x.z * c1 - x.w * s1,
-                     x.w * c1 + x.z * s1);
-}
-
 // Lazy-rescale threshold in log2 units: unnormalised probabilities stay below 2^kTau (fp16-safe).
 constexpr float kTau = 8.0f;
 // s_waitcnt operand (GFX9 encoding) waiting for all vector memory operations: vmcnt(0),
@@ -50,11 +42,13 @@ __device__ __forceinline__ int k_offset(int r, int c) { return r * 128 + ((c ^ (
 
 // Chunked V^T tile (time kernel): row d holds the 64 keys of channel d, and the 16-byte chunk
 // ks*4 + grp holds keys ks*32 + {grp*4 + i, 16 + grp*4 + i} (i = 0..3) in that order, so one
-// chunk is exactly one lane's A operand of O^T = V^T.P^T. Chunks are XOR-swizzled by d & 7.
+// chunk is exactly one lane's A operand of O^T = V^T.P^T. Chunks are XOR-swizzled by
+// (d ^ d >> 2) & 7, which differs across 8 consecutive rows (the operand reads) and across rows
+// 4 apart (the transposing writes of the staging threads).
 __device__ __forceinline__ int vtc_offset(int d, int key) {
   const int chunk = (key >> 5) * 4 + ((key & 15) >> 2);
   const int elem = (key & 3) + ((key & 16) >> 2);
-  return d * 128 + ((chunk ^ (d & 7)) << 4) + elem * 2;
+  return d * 128 + ((chunk ^ ((d ^ (d >> 2)) & 7)) << 4) + elem * 2;
 }
 
 // B operand of O^T = V^T.P^T from the score tiles of key blocks 2ks and 2ks+1.
@@ -171,7 +165,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   const unsigned voff = (unsigned)(2 * lrow) * ldv4 + lchunk * 16;
   const unsigned toff = (unsigned)lrow * 256 + lchunk * 16;
   float4 kreg[2], vreg[2];
-  float2 kcos[2], ksin[2];
+  float4 kcos[2], ksin[2];
   auto load_tile = [&](int key0) {
     const unsigned rows = (unsigned)(T - key0);
     const rsrc_t kr = make_rsrc(kbase + (long)key0 * p.ldk, (rows - 1) * ldk4 + 256);
@@ -187,8 +181,8 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
 #pragma unroll
       for (int it = 0; it < 2; it++) {
         const unsigned o = toff + it * 32 * 256;
-        kcos[it] = make_float2(bload1(cr, o), bload1(cr, o + 8));
-        ksin[it] = make_float2(bload1(sr, o + 4), bload1(sr, o + 12));
+        kcos[it] = bload4<ALIGNED>(cr, o);
+        ksin[it] = bload4<ALIGNED>(sr, o);
       }
     }
   };
@@ -197,7 +191,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
     for (int it = 0; it < 2; it++) {
       const int r = lrow + 32 * it;
       float4 x = kreg[it];
-      if constexpr (ROPE) x = rotate_pairs(x, kcos[it].x, kcos[it].y, ksin[it].x, ksin[it].y);
+      if constexpr (ROPE) x = rotate4(x, kcos[it], ksin[it]);
       const u32x2 w = {pack_h2(x.x, x.y), pack_h2(x.z, x.w)};
       *reinterpret_cast<u32x2*>(lds_k[buf] + k_offset(r, lchunk >> 1) + ((lchunk & 1) << 3)) = w;
     }
@@ -210,7 +204,8 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   };
 
   f32x4 o[4][4];
-  float lsum[4];
+  f32x4 lsum[4];
+  const u32x4 ones = {kOnesH2, kOnesH2, kOnesH2, kOnesH2};
   // Running maximum per query block (log2 units). Scores come out of the MFMA as s - m
   // because the S accumulators are seeded with -m.
   float m[4];
@@ -218,7 +213,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   for (int qb = 0; qb < 4; qb++) {
 #pragma unroll
     for (int db = 0; db < 4; db++) o[db][qb] = zero4();
-    lsum[qb] = 0.f;
+    lsum[qb] = zero4();
   }
 
   const int ntiles = (T + 63) / 64;
@@ -253,8 +248,10 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   // Fragment rows are 16*x + col, so the chunk swizzle depends on col only: one per-lane base
   // per channel step ds (K and Q) or key step ks (V^T), plus compile-time row offsets.
   const int kq_base[2] = {k_offset(col, grp), k_offset(col, 4 + grp)};
-  const int v_base[2] = {col * 128 + ((grp ^ (col & 7)) << 4),
-                         col * 128 + (((4 + grp) ^ (col & 7)) << 4)};
+  const int vsw = (col ^ (col >> 2)) & 7;
+  const int v_base[2][2] = {{col * 128 + ((grp ^ vsw) << 4), col * 128 + ((grp ^ vsw ^ 4) << 4)},
+                            {col * 128 + (((4 + grp) ^ vsw) << 4),
+                             col * 128 + (((4 + grp) ^ vsw ^ 4) << 4)}};
   auto q_frag = [&](int qb, int ds) {
     return *reinterpret_cast<const u32x4*>(Q + kq_base[ds] + qb * 2048);
   };
@@ -262,7 +259,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
     return *reinterpret_cast<const u32x4*>(K + kq_base[ds] + (half * 2 + kb2) * 2048);
   };
   auto v_frag = [&](const unsigned char* V, int ks, int db) {
-    return *reinterpret_cast<const u32x4*>(V + v_base[ks] + db * 2048);
+    return *reinterpret_cast<const u32x4*>(V + v_base[ks][db & 1] + db * 2048);
   };
   // S^T block of 32 keys (half) x 16 queries (qb): acc[kb2][r] = S[key (half*2+kb2)*16 +
   // grp*4 + r][query qb*16 + col] + init.
@@ -342,7 +339,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
         m[qb] += cm;
 #pragma unroll
         for (int kb = 0; kb < 4; kb++) acc[kb] -= cm;
-        lsum[qb] *= alpha;
+        scale_in_place(lsum[qb], alpha);
 #pragma unroll
         for (int db = 0; db < 4; db++) scale_in_place(o[db][qb], alpha);
       }
@@ -377,10 +374,8 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
 #pragma unroll
         for (int r = 0; r < 4; r++) sa[kb][r] = fast_exp2(sa[kb][r]);
       const u32x4 pf0 = p_fragment(sa[0], sa[1]), pf1 = p_fragment(sa[2], sa[3]);
-      lsum[u] += (((sa[0][0] + sa[0][1]) + (sa[0][2] + sa[0][3])) +
-                  ((sa[1][0] + sa[1][1]) + (sa[1][2] + sa[1][3]))) +
-                 (((sa[2][0] + sa[2][1]) + (sa[2][2] + sa[2][3])) +
-                  ((sa[3][0] + sa[3][1]) + (sa[3][2] + sa[3][3])));
+      lsum[u] = mfma16x16x32(ones, pf0, lsum[u]);
+      lsum[u] = mfma16x16x32(ones, pf1, lsum[u]);
       if (u + 1 < 4) {
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -419,7 +414,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
 #pragma unroll
     for (int qb = 0; qb < 4; qb++) {
       const f32x4 oq[4] = {o[0][qb], o[1][qb], o[2][qb], o[3][qb]};
-      store_output<GATED, ALIGNED>(out, oq, sum_over_rows(lsum[qb]), q0 + qb * 16 + col, grp);
+      store_output<GATED, ALIGNED>(out, oq, lsum[qb][0], q0 + qb * 16 + col, grp);
     }
   }
 }
@@ -491,8 +486,10 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   const int q0 = wave * 16;
   if (q0 >= T) return;
   const int kq_base[2] = {k_offset(col, grp), k_offset(col, 4 + grp)};
-  const int v_base[2] = {col * 128 + ((grp ^ (col & 7)) << 4),
-                         col * 128 + (((4 + grp) ^ (col & 7)) << 4)};
+  const int vsw = (col ^ (col >> 2)) & 7;
+  const int v_base[2][2] = {{col * 128 + ((grp ^ vsw) << 4), col * 128 + ((grp ^ vsw ^ 4) << 4)},
+                            {col * 128 + (((4 + grp) ^ vsw) << 4),
+                             col * 128 + (((4 + grp) ^ vsw ^ 4) << 4)}};
   const u32x4 qf[2] = {*reinterpret_cast<const u32x4*>(lds_q + kq_base[0] + wave * 2048),
                        *reinterpret_cast<const u32x4*>(lds_q + kq_base[1] + wave * 2048)};
   f32x4 s[4];
@@ -528,7 +525,7 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   for (int ks = 0; ks < 2; ks++) {
 #pragma unroll
     for (int db = 0; db < 4; db++)
-      o[db] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_v + v_base[ks] + db * 2048),
+      o[db] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_v + v_base[ks][db & 1] + db * 2048),
                            pf[ks], o[db]);
     lsum = mfma16x16x32(ones, pf[ks], lsum);
   }

@@ -39,14 +39,10 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Max / sum over the four lanes {l, l^16, l^32, l^48} that share a column of an MFMA tile.
+// Maximum over the four lanes {l, l^16, l^32, l^48} that share a column of an MFMA tile.
 __device__ __forceinline__ float max_over_rows(float x) {
   x = fmaxf(x, __shfl_xor(x, 16));
   return fmaxf(x, __shfl_xor(x, 32));
-}
-__device__ __forceinline__ float sum_over_rows(float x) {
-  x += __shfl_xor(x, 16);
-  return x + __shfl_xor(x, 32);
 }
 
 // Bijection from the hardware workgroup id to a logical id such that each XCD runs one
