@@ -5,13 +5,15 @@
 // written by one GEMM and read by the next is bit-for-bit the operand the next GEMM would
 // round to; only the bytes moved change.
 //
-// Workgroup = 4 waves, 128 x 128 output tile, 64 x 64 per wave (4 x 4 MFMA 16x16x32 tiles),
-// K in 64-wide steps through a double-buffered LDS tile, as in linear.hip. With fp16 x, global
-// loads run two K steps ahead (two register sets, used alternately), so each load has two steps
-// of MFMA work and barriers to arrive before it is needed; fp32 x keeps one step (its tiles
-// need twice the registers, and two workgroups per CU hide more than a second set would). Loads past the end of K or of the rows are given
-// an offset outside the buffer: they return 0 without touching memory, and the loop issues the
-// same loads every step (no conditional loads, so the compiler's wait counts stay exact).
+// Persistent workgroups (two per CU) walk 128 x 128 output tiles; each XCD takes one
+// contiguous range of tiles, column tiles of a row block next to each other, so a row block of
+// x is read from HBM once and re-read from that XCD's L2. Per tile: 4 waves, 64 x 64 each (4 x 4
+// MFMA 16x16x32 tiles), K in 64-wide steps through a double-buffered LDS tile, global loads one
+// step ahead in registers. After the last K step the accumulators go to LDS, and the loads of
+// the next tile's first step are issued before the epilogue, so they travel while the epilogue
+// reads the tile back row-wise (bias, GELU, rotary, residual: 512-byte coalesced rows) and
+// stores it. Loads past the end of K or of the rows get an offset outside the buffer: they
+// return 0 without touching memory.
 #include "buffer.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
@@ -24,6 +26,7 @@ using namespace gemm;
 
 // Offset added to a load that must read 0 (beyond every buffer range used here: < 2^31).
 constexpr unsigned kNowhere = 0x80000000u;
+constexpr int kStageFloats = kBM * kBN;  // epilogue staging: the fp32 output tile (64 KB)
 
 template <bool XH>
 struct XStage;  // registers holding one 128 x 64 x tile
@@ -41,24 +44,29 @@ struct WStage {  // fp16 W^T: 4 rows (output columns) x 8 halves per thread
   u32x4 v[4];
 };
 
+// Byte offset of float4 chunk c (columns 4c..4c+3) of row r in the [128][128] fp32 staging tile;
+// chunks are XOR-swizzled by r & 7 so 16 rows written at one chunk hit distinct banks.
+__device__ __forceinline__ int stage_offset(int r, int c) { return r * 512 + ((c ^ (r & 7)) << 4); }
+
 template <bool XH, bool OH, bool NORM>
-__global__ __launch_bounds__(kThreads, XH ? 1 : 2) void gemm16_kernel(Gemm16Params p, int col_tiles) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds_x[2][kTileBytes];
-  __shared__ __attribute__((aligned(16))) unsigned char lds_w[2][kTileBytes];
+__global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int col_tiles,
+                                                             int tiles) {
+  static_assert(4 * kTileBytes == kStageFloats * 4, "staging tile must fit the LDS pool");
+  __shared__ __attribute__((aligned(16))) unsigned char lds[4 * kTileBytes];
   __shared__ float lds_inv[kBM];
+  // K-step buffers: x tile b at lds + b*kTileBytes, W^T tile b at lds + (2+b)*kTileBytes.
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int tile = xcd_remap(blockIdx.x, gridDim.x);
-  const int r0 = (tile / col_tiles) * kBM, c0 = (tile % col_tiles) * kBN;
-  const int rows = min(kBM, p.n - r0);
   const int n = p.n, k = p.k, m = p.m;
   constexpr int xbytes = XH ? 2 : 4;
-
-  const rsrc_t xr = make_rsrc(static_cast<const unsigned char*>(p.x) + (long)r0 * p.ldx * xbytes,
-                              (unsigned)(((long)(rows - 1) * p.ldx + k) * xbytes));
-  const rsrc_t wr = make_rsrc(p.wt + (long)c0 * k, (unsigned)((long)min(kBN, m - c0) * k * 2));
   const unsigned ldx_b = (unsigned)p.ldx * xbytes, k2 = (unsigned)k * 2;
   const int ktiles = (k + kBK - 1) / kBK;
+
+  // Tiles of this workgroup: XCD x (= blockIdx % 8) owns tiles [x*per, (x+1)*per); its
+  // workgroups take every (gridDim/8)-th tile of that range.
+  const int xcd = blockIdx.x % kXcds, slot = blockIdx.x / kXcds, slots = gridDim.x / kXcds;
+  const int per = (tiles + kXcds - 1) / kXcds;
+  const int first = xcd * per + slot, last = min((xcd + 1) * per, tiles);
 
   // Staging roles: fp32 x: 16 lanes per row (float4), rows xr32 + 16i; fp16 x and W^T: 8 lanes
   // per row (8 halves), rows r16 + 32i.
@@ -66,34 +74,40 @@ __global__ __launch_bounds__(kThreads, XH ? 1 : 2) void gemm16_kernel(Gemm16Para
   const int c8 = tid & 7, r16 = tid >> 3;
 
   float ss[8];
-  if constexpr (NORM)
-    for (int i = 0; i < 8; i++) ss[i] = 0.f;
-
-  auto load = [&](XStage<XH>& xs, WStage& ws, int t) {
+  XStage<XH> xs;
+  WStage ws;
+  // Loads K step t of tile `tile` (tile >= last: nothing; every load returns 0).
+  auto load = [&](int tile, int t) {
+    const bool live = tile < last;
+    const int r0 = live ? (tile / col_tiles) * kBM : 0, c0 = live ? (tile % col_tiles) * kBN : 0;
+    const int rows = live ? min(kBM, n - r0) : 0;
+    const rsrc_t xr = make_rsrc(static_cast<const unsigned char*>(p.x) + (long)r0 * p.ldx * xbytes,
+                                rows ? (unsigned)(((long)(rows - 1) * p.ldx + k) * xbytes) : 0u);
+    const rsrc_t wr = make_rsrc(p.wt + (long)c0 * k, live ? (unsigned)((long)kBN * k * 2) : 0u);
     const int k0 = t * kBK;
     if constexpr (XH) {
       const int kc = k0 + 8 * c8;
-      const unsigned skip = (t < ktiles && kc < k) ? 0u : kNowhere;
+      const unsigned skip = kc < k ? 0u : kNowhere;
       for (int i = 0; i < 4; i++)
         xs.v[i] = __builtin_amdgcn_raw_buffer_load_b128(
             xr, ((unsigned)(r16 + 32 * i) * ldx_b + kc * 2) | skip, 0, 0);
     } else {
       const int kc = k0 + 4 * x4;
-      const unsigned skip = (t < ktiles && kc < k) ? 0u : kNowhere;
+      const unsigned skip = kc < k ? 0u : kNowhere;
       for (int i = 0; i < 8; i++)
         xs.v[i] = __builtin_bit_cast(
             float4, __builtin_amdgcn_raw_buffer_load_b128(
                         xr, ((unsigned)(xr32 + 16 * i) * ldx_b + kc * 4) | skip, 0, 0));
     }
     const int kc = k0 + 8 * c8;
-    const unsigned skip = (t < ktiles && kc < k) ? 0u : kNowhere;
+    const unsigned skip = kc < k ? 0u : kNowhere;
     for (int i = 0; i < 4; i++)
       ws.v[i] = __builtin_amdgcn_raw_buffer_load_b128(
           wr, ((unsigned)(r16 + 32 * i) * k2 + kc * 2) | skip, 0, 0);
   };
-  auto store = [&](const XStage<XH>& xs, const WStage& ws, int buf) {
-    unsigned char* X = lds_x[buf];
-    unsigned char* Wt = lds_w[buf];
+  auto store = [&](int buf) {
+    unsigned char* X = lds + buf * kTileBytes;
+    unsigned char* Wt = lds + (2 + buf) * kTileBytes;
     if constexpr (XH) {
       for (int i = 0; i < 4; i++) {
         if constexpr (NORM) {
@@ -119,12 +133,9 @@ __global__ __launch_bounds__(kThreads, XH ? 1 : 2) void gemm16_kernel(Gemm16Para
   const int qr = (wave & 1) * 64, qc = (wave >> 1) * 64;
   const int lr = lane & 15, lk = lane >> 4;
   f32x4 acc[4][4];
-  for (int a = 0; a < 4; a++)
-    for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-
   auto compute = [&](int buf) {
-    const unsigned char* X = lds_x[buf];
-    const unsigned char* Wt = lds_w[buf];
+    const unsigned char* X = lds + buf * kTileBytes;
+    const unsigned char* Wt = lds + (2 + buf) * kTileBytes;
     for (int kk = 0; kk < 2; kk++) {
       u32x4 a[4], b[4];
       for (int cb = 0; cb < 4; cb++)
@@ -136,86 +147,78 @@ __global__ __launch_bounds__(kThreads, XH ? 1 : 2) void gemm16_kernel(Gemm16Para
     }
   };
 
-  XStage<XH> x0;
-  WStage w0;
-  load(x0, w0, 0);
-  if constexpr (XH) {
-    // fp16 x: two register sets, loads two K steps ahead.
-    XStage<XH> x1;
-    WStage w1;
-    load(x1, w1, 1);
-    store(x0, w0, 0);
-    __syncthreads();
-    load(x0, w0, 2);
-    for (int t = 0; t < ktiles; t += 2) {
-      // Tile t is in LDS buffer 0; registers: set 1 = tile t+1, set 0 = tile t+2 (in flight).
-      compute(0);
-      store(x1, w1, 1);
-      __syncthreads();
-      load(x1, w1, t + 3);
-      if (t + 1 >= ktiles) break;
-      compute(1);
-      store(x0, w0, 0);
-      __syncthreads();
-      load(x0, w0, t + 4);
-    }
-  } else {
-    // fp32 x (twice the register bytes per tile): one register set, loads one K step ahead,
-    // which keeps two workgroups per CU.
-    store(x0, w0, 0);
-    __syncthreads();
-    load(x0, w0, 1);
-    for (int t = 0; t < ktiles; t++) {
-      compute(t & 1);
-      store(x0, w0, (t + 1) & 1);
-      __syncthreads();
-      load(x0, w0, t + 2);
-    }
-  }
-
-  if constexpr (NORM) {
-    // Per-row sums of squares: partials of the lanes sharing a row, then one value per row.
-    constexpr int kRowsPerThread = XH ? 4 : 8;
-    constexpr int kLanesPerRow = XH ? 8 : 16;
-    for (int i = 0; i < kRowsPerThread; i++) {
-      float s = ss[i];
-      for (int o = 1; o < kLanesPerRow; o <<= 1) s += __shfl_xor(s, o);
-      const int row = XH ? r16 + 32 * i : xr32 + 16 * i;
-      if ((XH ? c8 : x4) == 0) lds_inv[row] = 1.0f / fmaxf(sqrtf(s), 1e-12f);
-    }
-    __syncthreads();
-  }
-
-  // Epilogue: bias -> GELU -> rotary -> residual (fused/gemm.rs:46-82 order).
-  constexpr int obytes = OH ? 2 : 4;
-  const rsrc_t outr = make_rsrc(static_cast<unsigned char*>(p.out) + (long)r0 * m * obytes,
-                                (unsigned)((long)rows * m * obytes));
-  const rsrc_t resr = make_rsrc(p.residual ? p.residual + (long)r0 * m : p.bias,
-                                p.residual ? (unsigned)((long)rows * m * 4) : 0u);
-  const rsrc_t biasr = make_rsrc(p.bias ? p.bias : p.residual, p.bias ? (unsigned)m * 4 : 0u);
-  const rsrc_t roper = make_rsrc(p.rope ? p.rope : p.bias,
+  // Epilogue constants: this thread's 4 output columns (c4) in the row-wise pass.
+  const int c4 = tid & 31, erow = tid >> 5;
+  const void* any = p.wt;  // base of the empty descriptors of absent operands
+  const rsrc_t biasr = make_rsrc(p.bias ? static_cast<const void*>(p.bias) : any,
+                                 p.bias ? (unsigned)m * 4 : 0u);
+  const rsrc_t roper = make_rsrc(p.rope ? static_cast<const void*>(p.rope) : any,
                                  p.rope ? (unsigned)(4 * p.tokens * 64 * 4) : 0u);
-  for (int rb = 0; rb < 4; rb++) {
-    const int lrow = qr + rb * 16 + lr;
-    const int row = r0 + lrow;
-    const float inv = NORM ? lds_inv[lrow] : 1.0f;
-    const int tok = p.rope ? row % p.tokens : 0;
-    for (int cb = 0; cb < 4; cb++) {
-      const int col = c0 + qc + cb * 16 + 4 * lk;
-      if (row >= n) continue;
-      const f32x4 a = acc[cb][rb];
-      float4 v = make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
-      if (p.bias) {
-        const float4 b = bload4<true>(biasr, col * 4);
-        v = make_float4(v.x + b.x, v.y + b.y, v.z + b.z, v.w + b.w);
+
+  load(first, 0);
+  for (int tile = first; tile < last; tile += slots) {
+    const int r0 = (tile / col_tiles) * kBM, c0 = (tile % col_tiles) * kBN;
+    const int rows = min(kBM, n - r0);
+    if constexpr (NORM)
+      for (int i = 0; i < 8; i++) ss[i] = 0.f;
+    for (int a = 0; a < 4; a++)
+      for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    store(0);
+    __syncthreads();
+    for (int t = 0; t < ktiles; t++) {
+      // Next step of this tile, or the first step of the next tile (in flight over the epilogue).
+      if (t + 1 < ktiles)
+        load(tile, t + 1);
+      else
+        load(tile + slots, 0);
+      compute(t & 1);
+      if (t + 1 < ktiles) store((t + 1) & 1);
+      __syncthreads();
+    }
+    if constexpr (NORM) {
+      // Per-row sums of squares: partials of the lanes sharing a row, then one value per row.
+      constexpr int kRowsPerThread = XH ? 4 : 8;
+      constexpr int kLanesPerRow = XH ? 8 : 16;
+      for (int i = 0; i < kRowsPerThread; i++) {
+        float s = ss[i];
+        for (int o = 1; o < kLanesPerRow; o <<= 1) s += __shfl_xor(s, o);
+        const int row = XH ? r16 + 32 * i : xr32 + 16 * i;
+        if ((XH ? c8 : x4) == 0) lds_inv[row] = 1.0f / fmaxf(sqrtf(s), 1e-12f);
       }
+    }
+    // Accumulators -> LDS (the K-step buffers are free after the barrier above).
+    for (int rb = 0; rb < 4; rb++)
+      for (int cb = 0; cb < 4; cb++)
+        *reinterpret_cast<f32x4*>(lds + stage_offset(qr + rb * 16 + lr, (qc + cb * 16) / 4 + lk)) =
+            acc[cb][rb];
+    __syncthreads();
+
+    // Row-wise epilogue: bias -> GELU -> rotary -> residual (fused/gemm.rs:46-82 order).
+    constexpr int obytes = OH ? 2 : 4;
+    const rsrc_t outr = make_rsrc(static_cast<unsigned char*>(p.out) + (long)r0 * m * obytes,
+                                  (unsigned)((long)rows * m * obytes));
+    const rsrc_t resr = make_rsrc(p.residual ? static_cast<const void*>(p.residual + (long)r0 * m)
+                                             : any,
+                                  p.residual ? (unsigned)((long)rows * m * 4) : 0u);
+    const int col = c0 + 4 * c4;
+    float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (p.bias) bias = bload4<true>(biasr, col * 4);
+    const bool rot = p.rope && col < 2 * p.width;
+    const int table = col < p.width ? 0 : 2;
+    for (int i = 0; i < kBM / 8; i++) {
+      const int lrow = erow + 8 * i;
+      if (lrow >= rows) break;
+      const float4 a = *reinterpret_cast<const float4*>(lds + stage_offset(lrow, c4));
+      const float inv = NORM ? lds_inv[lrow] : 1.0f;
+      float4 v = make_float4(a.x * inv + bias.x, a.y * inv + bias.y, a.z * inv + bias.z,
+                             a.w * inv + bias.w);
       if (p.gelu) v = make_float4(gelu_erf(v.x), gelu_erf(v.y), gelu_erf(v.z), gelu_erf(v.w));
-      if (p.rope && col < 2 * p.width) {
-        const int table = col < p.width ? 0 : 2;
+      if (rot) {
+        const int tok = (r0 + lrow) % p.tokens;
         const unsigned c = ((unsigned)(table * p.tokens + tok) * 64 + (col & 63)) * 4;
         v = rotate4(v, bload4<true>(roper, c), bload4<true>(roper, c + (unsigned)p.tokens * 256));
       }
-      const unsigned off = (unsigned)lrow * m + col;  // element offset inside the tile rows
+      const unsigned off = (unsigned)lrow * m + col;
       if (p.residual) {
         const float4 r = bload4<true>(resr, off * 4);
         v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
@@ -227,30 +230,51 @@ __global__ __launch_bounds__(kThreads, XH ? 1 : 2) void gemm16_kernel(Gemm16Para
         bstore4<true>(outr, off * 4, v);
       }
     }
+    __syncthreads();  // the staging tile is the next tile's K-step buffers
   }
 }
 
 template <bool XH, bool OH, bool NORM>
-void launch(const Gemm16Params& p, dim3 grid, int col_tiles, hipStream_t stream) {
-  hipLaunchKernelGGL((gemm16_kernel<XH, OH, NORM>), grid, dim3(kThreads), 0, stream, p,
-                     col_tiles);
+void launch(const Gemm16Params& p, int grid, int col_tiles, int tiles, hipStream_t stream) {
+  hipLaunchKernelGGL((gemm16_kernel<XH, OH, NORM>), dim3(grid), dim3(kThreads), 0, stream, p,
+                     col_tiles, tiles);
+}
+
+// Compute units of the current device (cached per device).
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!cached[dev]) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
 }
 
 }  // namespace
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream) {
   const int row_tiles = (p.n + kBM - 1) / kBM, col_tiles = p.m / kBN;
-  const dim3 grid(row_tiles * col_tiles);
+  const int tiles = row_tiles * col_tiles;
+  // Two resident workgroups per CU, a multiple of the XCD count, no more than the tiles need.
+  int grid = 2 * device_cus();
+  const int need = (tiles + kXcds - 1) / kXcds * kXcds;
+  grid = (grid < need ? grid : need) / kXcds * kXcds;
+  if (grid < kXcds) grid = kXcds;
   const int key = (p.x_half ? 4 : 0) | (p.out_half ? 2 : 0) | (p.norm ? 1 : 0);
   switch (key) {
-    case 0: launch<false, false, false>(p, grid, col_tiles, stream); break;
-    case 1: launch<false, false, true>(p, grid, col_tiles, stream); break;
-    case 2: launch<false, true, false>(p, grid, col_tiles, stream); break;
-    case 3: launch<false, true, true>(p, grid, col_tiles, stream); break;
-    case 4: launch<true, false, false>(p, grid, col_tiles, stream); break;
-    case 5: launch<true, false, true>(p, grid, col_tiles, stream); break;
-    case 6: launch<true, true, false>(p, grid, col_tiles, stream); break;
-    default: launch<true, true, true>(p, grid, col_tiles, stream); break;
+    case 0: launch<false, false, false>(p, grid, col_tiles, tiles, stream); break;
+    case 1: launch<false, false, true>(p, grid, col_tiles, tiles, stream); break;
+    case 2: launch<false, true, false>(p, grid, col_tiles, tiles, stream); break;
+    case 3: launch<false, true, true>(p, grid, col_tiles, tiles, stream); break;
+    case 4: launch<true, false, false>(p, grid, col_tiles, tiles, stream); break;
+    case 5: launch<true, false, true>(p, grid, col_tiles, tiles, stream); break;
+    case 6: launch<true, true, false>(p, grid, col_tiles, tiles, stream); break;
+    default: launch<true, true, true>(p, grid, col_tiles, tiles, stream); break;
   }
   return hipGetLastError();
 }
