@@ -7,8 +7,8 @@
 //
 // Persistent workgroups (two per CU) walk 128 x 128 output tiles; each XCD takes one
 // contiguous range of tiles, column tiles of a row block next to each other, so a row block of
-// x is read from HBM once and re-read from that XCD's L2. Per tile: 4 waves, 64 x 64 each (4 x 4
-// MFMA 16x16x32 tiles), K in 64-wide steps through a double-buffered LDS tile, global loads one
+// x is read from HBM once and re-read from that XCD's L2. Per tile: 4 waves of 64 x 64 (fp16 x)
+// or 8 waves of 64 x 32 (fp32 x) in MFMA 16x16x32 tiles, K in 64-wide steps through a double-buffered LDS tile, global loads one
 // step ahead in registers. After the last K step the accumulators go to LDS, and the loads of
 // the next tile's first step are issued before the epilogue, so they travel while the epilogue
 // reads the tile back row-wise (bias, GELU, rotary, residual: 512-byte coalesced rows) and
@@ -28,29 +28,38 @@ using namespace gemm;
 constexpr unsigned kNowhere = 0x80000000u;
 constexpr int kStageFloats = kBM * kBN;  // epilogue staging: the fp32 output tile (64 KB)
 
-template <bool XH>
-struct XStage;  // registers holding one 128 x 64 x tile
-
-template <>
-struct XStage<false> {  // fp32 x: 8 rows x float4 per thread
-  float4 v[8];
+// Registers of one 128 x 64 x tile and one 128 x 64 W^T tile, spread over NT threads: fp32 x
+// as float4 (16 threads per row), fp16 x and W^T as 8 halves (8 threads per row).
+template <bool XH, int NT>
+struct XStage;
+template <int NT>
+struct XStage<false, NT> {
+  float4 v[2048 / NT];
 };
-template <>
-struct XStage<true> {  // fp16 x: 4 rows x 8 halves per thread
-  u32x4 v[4];
+template <int NT>
+struct XStage<true, NT> {
+  u32x4 v[1024 / NT];
 };
-
-struct WStage {  // fp16 W^T: 4 rows (output columns) x 8 halves per thread
-  u32x4 v[4];
+template <int NT>
+struct WStage {
+  u32x4 v[1024 / NT];
 };
 
 // Byte offset of float4 chunk c (columns 4c..4c+3) of row r in the [128][128] fp32 staging tile;
 // chunks are XOR-swizzled by r & 7 so 16 rows written at one chunk hit distinct banks.
 __device__ __forceinline__ int stage_offset(int r, int c) { return r * 512 + ((c ^ (r & 7)) << 4); }
 
-template <bool XH, bool OH, bool NORM>
-__global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int col_tiles,
-                                                             int tiles) {
+// WAVES = 4 (64 x 64 per wave) or 8 (64 x 32 per wave: half the accumulators and staging
+// registers per thread, which the fp32-input variants need to stay within 128 registers).
+template <bool XH, bool OH, bool NORM, int WAVES>
+__global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, int col_tiles,
+                                                               int tiles) {
+  constexpr int NT = WAVES * 64;
+  constexpr int XP = XH ? 1024 / NT : 2048 / NT;  // x rows per thread per K step
+  constexpr int WP = 1024 / NT;                   // W^T rows per thread per K step
+  constexpr int CB = WAVES == 4 ? 4 : 2;          // 16-column MFMA blocks per wave
+  constexpr int XROWS = XH ? NT / 8 : NT / 16;    // x rows covered per pass
+  constexpr int WROWS = NT / 8;
   static_assert(4 * kTileBytes == kStageFloats * 4, "staging tile must fit the LDS pool");
   __shared__ __attribute__((aligned(16))) unsigned char lds[4 * kTileBytes];
   __shared__ float lds_inv[kBM];
@@ -68,14 +77,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int
   const int per = (tiles + kXcds - 1) / kXcds;
   const int first = xcd * per + slot, last = min((xcd + 1) * per, tiles);
 
-  // Staging roles: fp32 x: 16 lanes per row (float4), rows xr32 + 16i; fp16 x and W^T: 8 lanes
-  // per row (8 halves), rows r16 + 32i.
+  // Staging roles: fp32 x: 16 lanes per row (float4), rows xr32 + XROWS*i; fp16 x and W^T:
+  // 8 lanes per row (8 halves), rows r16 + XROWS*i (x) or r16 + WROWS*i (W^T).
   const int x4 = tid & 15, xr32 = tid >> 4;
   const int c8 = tid & 7, r16 = tid >> 3;
 
-  float ss[8];
-  XStage<XH> xs;
-  WStage ws;
+  float ss[XP];
+  XStage<XH, NT> xs;
+  WStage<NT> ws;
   // Loads K step t of tile `tile` (tile >= last: nothing; every load returns 0).
   auto load = [&](int tile, int t) {
     const bool live = tile < last;
@@ -88,61 +97,62 @@ __global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int
     if constexpr (XH) {
       const int kc = k0 + 8 * c8;
       const unsigned skip = kc < k ? 0u : kNowhere;
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < XP; i++)
         xs.v[i] = __builtin_amdgcn_raw_buffer_load_b128(
-            xr, ((unsigned)(r16 + 32 * i) * ldx_b + kc * 2) | skip, 0, 0);
+            xr, ((unsigned)(r16 + XROWS * i) * ldx_b + kc * 2) | skip, 0, 0);
     } else {
       const int kc = k0 + 4 * x4;
       const unsigned skip = kc < k ? 0u : kNowhere;
-      for (int i = 0; i < 8; i++)
+      for (int i = 0; i < XP; i++)
         xs.v[i] = __builtin_bit_cast(
             float4, __builtin_amdgcn_raw_buffer_load_b128(
-                        xr, ((unsigned)(xr32 + 16 * i) * ldx_b + kc * 4) | skip, 0, 0));
+                        xr, ((unsigned)(xr32 + XROWS * i) * ldx_b + kc * 4) | skip, 0, 0));
     }
     const int kc = k0 + 8 * c8;
     const unsigned skip = kc < k ? 0u : kNowhere;
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < WP; i++)
       ws.v[i] = __builtin_amdgcn_raw_buffer_load_b128(
-          wr, ((unsigned)(r16 + 32 * i) * k2 + kc * 2) | skip, 0, 0);
+          wr, ((unsigned)(r16 + WROWS * i) * k2 + kc * 2) | skip, 0, 0);
   };
   auto store = [&](int buf) {
     unsigned char* X = lds + buf * kTileBytes;
     unsigned char* Wt = lds + (2 + buf) * kTileBytes;
     if constexpr (XH) {
-      for (int i = 0; i < 4; i++) {
+      for (int i = 0; i < XP; i++) {
         if constexpr (NORM) {
           const h16x8 h = __builtin_bit_cast(h16x8, xs.v[i]);
           float s = 0.f;
           for (int j = 0; j < 8; j++) s += (float)h[j] * (float)h[j];
           ss[i] += s;
         }
-        *reinterpret_cast<u32x4*>(X + tile_offset(r16 + 32 * i, c8)) = xs.v[i];
+        *reinterpret_cast<u32x4*>(X + tile_offset(r16 + XROWS * i, c8)) = xs.v[i];
       }
     } else {
-      for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < XP; i++) {
         const float4 v = xs.v[i];
         if constexpr (NORM) ss[i] += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
         const u32x2 h = {pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
-        *reinterpret_cast<u32x2*>(X + tile_offset(xr32 + 16 * i, x4 >> 1) + ((x4 & 1) << 3)) = h;
+        *reinterpret_cast<u32x2*>(X + tile_offset(xr32 + XROWS * i, x4 >> 1) + ((x4 & 1) << 3)) =
+            h;
       }
     }
-    for (int i = 0; i < 4; i++)
-      *reinterpret_cast<u32x4*>(Wt + tile_offset(r16 + 32 * i, c8)) = ws.v[i];
+    for (int i = 0; i < WP; i++)
+      *reinterpret_cast<u32x4*>(Wt + tile_offset(r16 + WROWS * i, c8)) = ws.v[i];
   };
 
-  const int qr = (wave & 1) * 64, qc = (wave >> 1) * 64;
+  const int qr = (wave & 1) * 64, qc = (wave >> 1) * 16 * CB;
   const int lr = lane & 15, lk = lane >> 4;
-  f32x4 acc[4][4];
+  f32x4 acc[CB][4];
   auto compute = [&](int buf) {
     const unsigned char* X = lds + buf * kTileBytes;
     const unsigned char* Wt = lds + (2 + buf) * kTileBytes;
     for (int kk = 0; kk < 2; kk++) {
-      u32x4 a[4], b[4];
-      for (int cb = 0; cb < 4; cb++)
+      u32x4 a[CB], b[4];
+      for (int cb = 0; cb < CB; cb++)
         a[cb] = *reinterpret_cast<const u32x4*>(Wt + tile_offset(qc + cb * 16 + lr, kk * 4 + lk));
       for (int rb = 0; rb < 4; rb++)
         b[rb] = *reinterpret_cast<const u32x4*>(X + tile_offset(qr + rb * 16 + lr, kk * 4 + lk));
-      for (int cb = 0; cb < 4; cb++)
+      for (int cb = 0; cb < CB; cb++)
         for (int rb = 0; rb < 4; rb++) acc[cb][rb] = mfma16x16x32(a[cb], b[rb], acc[cb][rb]);
     }
   };
@@ -160,8 +170,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int
     const int r0 = (tile / col_tiles) * kBM, c0 = (tile % col_tiles) * kBN;
     const int rows = min(kBM, n - r0);
     if constexpr (NORM)
-      for (int i = 0; i < 8; i++) ss[i] = 0.f;
-    for (int a = 0; a < 4; a++)
+      for (int i = 0; i < XP; i++) ss[i] = 0.f;
+    for (int a = 0; a < CB; a++)
       for (int b = 0; b < 4; b++) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     store(0);
     __syncthreads();
@@ -177,18 +187,17 @@ __global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int
     }
     if constexpr (NORM) {
       // Per-row sums of squares: partials of the lanes sharing a row, then one value per row.
-      constexpr int kRowsPerThread = XH ? 4 : 8;
       constexpr int kLanesPerRow = XH ? 8 : 16;
-      for (int i = 0; i < kRowsPerThread; i++) {
+      for (int i = 0; i < XP; i++) {
         float s = ss[i];
         for (int o = 1; o < kLanesPerRow; o <<= 1) s += __shfl_xor(s, o);
-        const int row = XH ? r16 + 32 * i : xr32 + 16 * i;
+        const int row = XH ? r16 + XROWS * i : xr32 + XROWS * i;
         if ((XH ? c8 : x4) == 0) lds_inv[row] = 1.0f / fmaxf(sqrtf(s), 1e-12f);
       }
     }
     // Accumulators -> LDS (the K-step buffers are free after the barrier above).
     for (int rb = 0; rb < 4; rb++)
-      for (int cb = 0; cb < 4; cb++)
+      for (int cb = 0; cb < CB; cb++)
         *reinterpret_cast<f32x4*>(lds + stage_offset(qr + rb * 16 + lr, (qc + cb * 16) / 4 + lk)) =
             acc[cb][rb];
     __syncthreads();
@@ -205,8 +214,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int
     if (p.bias) bias = bload4<true>(biasr, col * 4);
     const bool rot = p.rope && col < 2 * p.width;
     const int table = col < p.width ? 0 : 2;
-    for (int i = 0; i < kBM / 8; i++) {
-      const int lrow = erow + 8 * i;
+    for (int i = 0; i < kBM / (NT / 32); i++) {
+      const int lrow = erow + (NT / 32) * i;
       if (lrow >= rows) break;
       const float4 a = *reinterpret_cast<const float4*>(lds + stage_offset(lrow, c4));
       const float inv = NORM ? lds_inv[lrow] : 1.0f;
@@ -236,8 +245,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemm16_kernel(Gemm16Params p, int
 
 template <bool XH, bool OH, bool NORM>
 void launch(const Gemm16Params& p, int grid, int col_tiles, int tiles, hipStream_t stream) {
-  hipLaunchKernelGGL((gemm16_kernel<XH, OH, NORM>), dim3(grid), dim3(kThreads), 0, stream, p,
-                     col_tiles, tiles);
+  constexpr int waves = XH ? 4 : 8;
+  hipLaunchKernelGGL((gemm16_kernel<XH, OH, NORM, waves>), dim3(grid), dim3(waves * 64), 0,
+                     stream, p, col_tiles, tiles);
 }
 
 // Compute units of the current device (cached per device).
@@ -260,8 +270,10 @@ int device_cus() {
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream) {
   const int row_tiles = (p.n + kBM - 1) / kBM, col_tiles = p.m / kBN;
   const int tiles = row_tiles * col_tiles;
-  // Two resident workgroups per CU, a multiple of the XCD count, no more than the tiles need.
-  int grid = 2 * device_cus();
+  // Resident workgroups only (two 4-wave ones per CU for fp16 x; one 8-wave one for fp32 x,
+  // whose registers allow three waves per SIMD), a multiple of the XCD count, no more than the
+  // tiles need.
+  int grid = (p.x_half ? 2 : 1) * device_cus();
   const int need = (tiles + kXcds - 1) / kXcds * kXcds;
   grid = (grid < need ? grid : need) / kXcds * kXcds;
   if (grid < kXcds) grid = kXcds;
