@@ -57,6 +57,11 @@ __device__ __forceinline__ u32x4 p_fragment(f32x4 a, f32x4 b) {
                pack_h2(b[2], b[3])};
 }
 
+// First row of group g (token 0) in q/k/v/gate/out; token t adds t * p.tstep rows.
+__device__ __forceinline__ long group_row(const AttnParams& p, int g) {
+  return (long)(g / p.gsplit) * p.gouter + (long)(g % p.gsplit) * p.gstep;
+}
+
 // Output rows of one (group, head): [tokens, heads*64] starting at channel 64*h.
 struct OutRows {
   rsrc_t out, gate;
@@ -66,15 +71,15 @@ struct OutRows {
 
 __device__ __forceinline__ OutRows out_rows(const AttnParams& p, int g, int h) {
   const int T = p.tokens;
+  const long row = group_row(p, g);
   OutRows o;
   o.half = p.out_half != 0;
   const unsigned esize = o.half ? 2 : 4;
-  o.ld4 = (unsigned)p.heads * 64 * esize;
-  o.out = make_rsrc(reinterpret_cast<unsigned char*>(p.out) +
-                        ((long)g * T * p.heads + h) * 64 * esize,
+  o.ld4 = (unsigned)(p.tstep * p.heads * 64 * esize);
+  o.out = make_rsrc(reinterpret_cast<unsigned char*>(p.out) + (row * p.heads + h) * 64 * esize,
                     (unsigned)(T - 1) * o.ld4 + 64 * esize);
-  o.ldg4 = (unsigned)p.ldg * 4;
-  o.gate = make_rsrc(p.gate ? p.gate + (long)g * T * p.ldg + h : p.out,
+  o.ldg4 = (unsigned)(p.tstep * p.ldg * 4);
+  o.gate = make_rsrc(p.gate ? p.gate + row * p.ldg + h : p.out,
                      p.gate ? (unsigned)(T - 1) * o.ldg4 + 4 : 0);
   return o;
 }
@@ -146,10 +151,11 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   const int qblk = logical % qblocks, gh = logical / qblocks;
   const int h = gh % p.heads, g = gh / p.heads;
   const int T = p.tokens;
-  const unsigned ldq4 = (unsigned)p.ldq * 4, ldk4 = (unsigned)p.ldk * 4,
-                 ldv4 = (unsigned)p.ldv * 4;
-  const float* kbase = p.k + (long)g * T * p.ldk + h * 64;
-  const float* vbase = p.v + (long)g * T * p.ldv + h * 64;
+  const long row0 = group_row(p, g), ts = p.tstep;
+  const unsigned ldq4 = (unsigned)(ts * p.ldq * 4), ldk4 = (unsigned)(ts * p.ldk * 4),
+                 ldv4 = (unsigned)(ts * p.ldv * 4);
+  const float* kbase = p.k + row0 * p.ldk + h * 64;
+  const float* vbase = p.v + row0 * p.ldv + h * 64;
   const int q0 = qblk * kTimeQueries + wave * 64;
   const bool active = q0 < T;
 
@@ -168,8 +174,8 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   float4 kcos[2], ksin[2];
   auto load_tile = [&](int key0) {
     const unsigned rows = (unsigned)(T - key0);
-    const rsrc_t kr = make_rsrc(kbase + (long)key0 * p.ldk, (rows - 1) * ldk4 + 256);
-    const rsrc_t vr = make_rsrc(vbase + (long)key0 * p.ldv, (rows - 1) * ldv4 + 256);
+    const rsrc_t kr = make_rsrc(kbase + key0 * ts * p.ldk, (rows - 1) * ldk4 + 256);
+    const rsrc_t vr = make_rsrc(vbase + key0 * ts * p.ldv, (rows - 1) * ldv4 + 256);
 #pragma unroll
     for (int it = 0; it < 2; it++) kreg[it] = bload4<ALIGNED>(kr, koff + it * 32 * ldk4);
 #pragma unroll
@@ -222,7 +228,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
     // Stage this wave's 64 query rows: coalesced row loads (16 lanes per 256-byte row), RoPE
     // with the query table rows (carrying 1/sqrt(64)), log2(e), fp16, into the K-tile layout.
     const unsigned rows = (unsigned)(T - q0);
-    const rsrc_t qr = make_rsrc(p.q + ((long)g * T + q0) * p.ldq + h * 64, (rows - 1) * ldq4 + 256);
+    const rsrc_t qr = make_rsrc(p.q + (row0 + q0 * ts) * p.ldq + h * 64, (rows - 1) * ldq4 + 256);
     const rsrc_t cr = make_rsrc(ROPE ? p.rope + (long)q0 * 64 : p.q, ROPE ? rows * 256 : 0);
     const rsrc_t sr = make_rsrc(ROPE ? p.rope + (long)(T + q0) * 64 : p.q, ROPE ? rows * 256 : 0);
     const int chunk = lane & 15;
@@ -437,11 +443,12 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   const int prob = blockIdx.x;
   const int h = prob % p.heads, g = prob / p.heads;
   const int T = p.tokens;
-  const unsigned ldq4 = (unsigned)p.ldq * 4, ldk4 = (unsigned)p.ldk * 4,
-                 ldv4 = (unsigned)p.ldv * 4;
-  const rsrc_t qr = make_rsrc(p.q + (long)g * T * p.ldq + h * 64, (unsigned)(T - 1) * ldq4 + 256);
-  const rsrc_t kr = make_rsrc(p.k + (long)g * T * p.ldk + h * 64, (unsigned)(T - 1) * ldk4 + 256);
-  const rsrc_t vr = make_rsrc(p.v + (long)g * T * p.ldv + h * 64, (unsigned)(T - 1) * ldv4 + 256);
+  const long row0 = group_row(p, g), ts = p.tstep;
+  const unsigned ldq4 = (unsigned)(ts * p.ldq * 4), ldk4 = (unsigned)(ts * p.ldk * 4),
+                 ldv4 = (unsigned)(ts * p.ldv * 4);
+  const rsrc_t qr = make_rsrc(p.q + row0 * p.ldq + h * 64, (unsigned)(T - 1) * ldq4 + 256);
+  const rsrc_t kr = make_rsrc(p.k + row0 * p.ldk + h * 64, (unsigned)(T - 1) * ldk4 + 256);
+  const rsrc_t vr = make_rsrc(p.v + row0 * p.ldv + h * 64, (unsigned)(T - 1) * ldv4 + 256);
 
   // Staging: q / k rows srow + 16*it at channels 4*sc; v key pairs (2*(srow + 16*it), +1),
   // it < 2. Rows at or past T read as 0.
@@ -548,7 +555,14 @@ static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
-hipError_t launch_attention(const AttnParams& p, bool aligned, hipStream_t stream) {
+hipError_t launch_attention(const AttnParams& params, bool aligned, hipStream_t stream) {
+  AttnParams p = params;
+  if (p.gsplit == 0) {
+    p.gsplit = 1;
+    p.gouter = p.tokens;
+    p.gstep = 0;
+    p.tstep = 1;
+  }
   const bool gated = p.gate != nullptr, rope = p.rope != nullptr;
   if (aligned) {
     if (gated) return rope ? launch_attention_t<true, true, true>(p, stream)

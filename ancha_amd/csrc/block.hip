@@ -71,8 +71,9 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 
 // One block GEMM through the fp16-weight kernel.
 int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, size_t m,
-         const float* bias, bool gelu, const float* rope, size_t tokens, size_t width,
-         const float* residual, void* out, bool out_half, bool norm, hipStream_t stream) {
+         const float* bias, bool gelu, const float* rope, size_t tokens, size_t token_div,
+         size_t width, const float* residual, void* out, bool out_half, bool norm,
+         hipStream_t stream) {
   ancha::Gemm16Params p{};
   p.x = x;
   p.wt = wt;
@@ -85,6 +86,7 @@ int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, siz
   p.k = static_cast<int>(k);
   p.m = static_cast<int>(m);
   p.tokens = rope ? static_cast<int>(tokens) : 1;
+  p.token_div = rope ? static_cast<int>(token_div) : 1;
   p.width = rope ? static_cast<int>(width) : 0;
   p.gelu = gelu;
   p.norm = norm;
@@ -97,6 +99,89 @@ int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, siz
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 }  // namespace
+
+// Workspace regions: the packed projection (fp32 [rows, columns]; later the fp16 FF hidden
+// activation [rows, hidden]), the fp16 attention output [rows, inner], x + attention (fp32).
+static size_t region_packed(const ancha_hip_block* b, size_t rows) {
+  const size_t p = rows * b->columns * 4, h = rows * b->hidden * 2;
+  return round_up(p > h ? p : h, 256);
+}
+
+// Forward of one block over `groups` sequences of `tokens` rows. split 0: sequence g is rows
+// g*tokens .. g*tokens + tokens - 1. split > 0: the rows are a [batch, tokens, split] grid (the
+// time layout [batch, bands, frames] with tokens = bands, split = frames) and sequence
+// g = b*split + f is rows (b*tokens + t)*split + f: the band pass runs on the time layout, with
+// no transposed copy. Every stage but attention and the rotary epilogue is row-wise, so only
+// those two see the layout. out may be x (x is last read before out is first written).
+static int block_forward(const ancha_hip_block* b, const float* x, size_t groups, size_t tokens,
+                         size_t split, const float* rope, void* workspace,
+                         size_t workspace_bytes, float* out, hipStream_t stream) {
+  if (!b) return ANCHA_HIP_INVALID;
+  const size_t rows = groups * tokens;
+  if (rows == 0) return ANCHA_HIP_OK;
+  if (!x || !out || !rope || !workspace) return ANCHA_HIP_INVALID;
+  if (workspace_bytes < ancha_hip_block_workspace(b, rows)) return ANCHA_HIP_INVALID;
+  if (!aligned16(x) || !aligned16(out) || !aligned16(rope) || !aligned16(workspace))
+    return ANCHA_HIP_INVALID;
+  if (split && groups % split) return ANCHA_HIP_INVALID;
+  if (rows > 0x7fffffff || rows * b->columns * 4 >= (size_t(1) << 40))
+    return ANCHA_HIP_UNSUPPORTED;
+  // Attention addresses one sequence with 32-bit offsets from its first row.
+  if (tokens * (split ? split : 1) * b->columns * 4 >= (size_t(1) << 31))
+    return ANCHA_HIP_UNSUPPORTED;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev != b->device) return ANCHA_HIP_INVALID;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  float* packed = reinterpret_cast<float*>(ws);                      // [rows, columns] fp32
+  _Float16* hidden = reinterpret_cast<_Float16*>(ws);                // [rows, hidden] fp16
+  _Float16* attended = reinterpret_cast<_Float16*>(ws + region_packed(b, rows));
+  float* x1 = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(attended) +
+                                       round_up(rows * b->inner * 2, 256));
+  const size_t dim = b->dim, inner = b->inner;
+  // packed = unit_norm(x) . [Wq|Wk|Wv|Wg|0] + [0|0|0|bg|0], RoPE on the q / k columns.
+  int rc = gemm(x, false, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
+                split ? split : 1, inner, nullptr, packed, false, true, stream);
+  if (rc) return rc;
+  // attended = softmax(q k^T) v * sigmoid(gate), stored fp16.
+  ancha::AttnParams ap{};
+  ap.q = packed;
+  ap.k = packed + inner;
+  ap.v = packed + 2 * inner;
+  ap.gate = packed + 3 * inner;
+  ap.out = reinterpret_cast<float*>(attended);
+  ap.ldq = ap.ldk = ap.ldv = ap.ldg = static_cast<long>(b->columns);
+  ap.groups = static_cast<int>(groups);
+  ap.tokens = static_cast<int>(tokens);
+  ap.heads = static_cast<int>(b->heads);
+  ap.out_half = 1;
+  if (split) {
+    ap.gsplit = static_cast<int>(split);
+    ap.gouter = static_cast<long>(tokens * split);
+    ap.gstep = 1;
+    ap.tstep = static_cast<long>(split);
+  } else {
+    ap.gsplit = 1;
+    ap.gouter = static_cast<long>(tokens);
+    ap.gstep = 0;
+    ap.tstep = 1;
+  }
+  hipError_t e = ancha::launch_attention(ap, true, stream);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  // x1 = x + attended . W_out
+  rc = gemm(attended, true, rows, inner, b->out_w, dim, nullptr, false, nullptr, 0, 1, 0, x, x1,
+            false, false, stream);
+  if (rc) return rc;
+  // hidden = GELU(unit_norm(x1) . W1' + b1), stored fp16.
+  rc = gemm(x1, false, rows, dim, b->ff_in_w, b->hidden, b->ff_in_b, true, nullptr, 0, 1, 0,
+            nullptr, hidden, true, true, stream);
+  if (rc) return rc;
+  // out = x1 + hidden . W2 + b2
+  rc = gemm(hidden, true, rows, b->hidden, b->ff_out_w, dim, b->ff_out_b, false, nullptr, 0, 1, 0,
+            x1, out, false, false, stream);
+  if (rc) return rc;
+  if (b->out_scale) rc = ancha_hip_unit_norm(out, rows, dim, dim, b->out_scale, out, stream);
+  return rc;
+}
 
 extern "C" {
 
@@ -163,13 +248,6 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
   return ANCHA_HIP_OK;
 }
 
-// Workspace regions: the packed projection (fp32 [rows, columns]; later the fp16 FF hidden
-// activation [rows, hidden]), the fp16 attention output [rows, inner], x + attention (fp32).
-static size_t region_packed(const ancha_hip_block* b, size_t rows) {
-  const size_t p = rows * b->columns * 4, h = rows * b->hidden * 2;
-  return round_up(p > h ? p : h, 256);
-}
-
 size_t ancha_hip_block_workspace(const ancha_hip_block* b, size_t rows) {
   if (!b) return 0;
   return region_packed(b, rows) + round_up(rows * b->inner * 2, 256) + rows * b->dim * 4;
@@ -178,63 +256,14 @@ size_t ancha_hip_block_workspace(const ancha_hip_block* b, size_t rows) {
 int ancha_hip_block_forward(const ancha_hip_block* b, const float* x, size_t groups,
                             size_t tokens, const float* rope, void* workspace,
                             size_t workspace_bytes, float* out, hipStream_t stream) {
-  if (!b) return ANCHA_HIP_INVALID;
-  const size_t rows = groups * tokens;
-  if (rows == 0) return ANCHA_HIP_OK;
-  if (!x || !out || !rope || !workspace) return ANCHA_HIP_INVALID;
-  if (workspace_bytes < ancha_hip_block_workspace(b, rows)) return ANCHA_HIP_INVALID;
-  if (!aligned16(x) || !aligned16(out) || !aligned16(rope) || !aligned16(workspace))
-    return ANCHA_HIP_INVALID;
-  if (rows > 0x7fffffff || rows * b->columns * 4 >= (size_t(1) << 40))
-    return ANCHA_HIP_UNSUPPORTED;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev != b->device) return ANCHA_HIP_INVALID;
-  unsigned char* ws = static_cast<unsigned char*>(workspace);
-  float* packed = reinterpret_cast<float*>(ws);                      // [rows, columns] fp32
-  _Float16* hidden = reinterpret_cast<_Float16*>(ws);                // [rows, hidden] fp16
-  _Float16* attended = reinterpret_cast<_Float16*>(ws + region_packed(b, rows));
-  float* x1 = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(attended) +
-                                       round_up(rows * b->inner * 2, 256));
-  const size_t dim = b->dim, inner = b->inner;
-  // packed = unit_norm(x) . [Wq|Wk|Wv|Wg|0] + [0|0|0|bg|0], RoPE on the q / k columns.
-  int rc = gemm(x, false, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
-                inner, nullptr, packed, false, true, stream);
-  if (rc) return rc;
-  // attended = softmax(q k^T) v * sigmoid(gate), stored fp16.
-  ancha::AttnParams ap{};
-  ap.q = packed;
-  ap.k = packed + inner;
-  ap.v = packed + 2 * inner;
-  ap.gate = packed + 3 * inner;
-  ap.out = reinterpret_cast<float*>(attended);
-  ap.ldq = ap.ldk = ap.ldv = ap.ldg = static_cast<long>(b->columns);
-  ap.groups = static_cast<int>(groups);
-  ap.tokens = static_cast<int>(tokens);
-  ap.heads = static_cast<int>(b->heads);
-  ap.out_half = 1;
-  hipError_t e = ancha::launch_attention(ap, true, stream);
-  if (e != hipSuccess) return -static_cast<int>(e);
-  // x1 = x + attended . W_out
-  rc = gemm(attended, true, rows, inner, b->out_w, dim, nullptr, false, nullptr, 0, 0, x, x1,
-            false, false, stream);
-  if (rc) return rc;
-  // hidden = GELU(unit_norm(x1) . W1' + b1), stored fp16.
-  rc = gemm(x1, false, rows, dim, b->ff_in_w, b->hidden, b->ff_in_b, true, nullptr, 0, 0, nullptr,
-            hidden, true, true, stream);
-  if (rc) return rc;
-  // out = x1 + hidden . W2 + b2
-  rc = gemm(hidden, true, rows, b->hidden, b->ff_out_w, dim, b->ff_out_b, false, nullptr, 0, 0,
-            x1, out, false, false, stream);
-  if (rc) return rc;
-  if (b->out_scale) rc = ancha_hip_unit_norm(out, rows, dim, dim, b->out_scale, out, stream);
-  return rc;
+  return block_forward(b, x, groups, tokens, 0, rope, workspace, workspace_bytes, out, stream);
 }
 
 size_t ancha_hip_axis_pair_workspace(const ancha_hip_block* time, const ancha_hip_block* band,
                                      size_t rows) {
   if (!time || !band || time->dim != band->dim) return 0;
   const size_t a = ancha_hip_block_workspace(time, rows), c = ancha_hip_block_workspace(band, rows);
-  return (a > c ? a : c) + 2 * rows * time->dim * sizeof(float);
+  return a > c ? a : c;
 }
 
 int ancha_hip_axis_pair_forward(const ancha_hip_block* time, const ancha_hip_block* band,
@@ -242,23 +271,17 @@ int ancha_hip_axis_pair_forward(const ancha_hip_block* time, const ancha_hip_blo
                                 const float* time_rope, const float* band_rope, void* workspace,
                                 size_t workspace_bytes, float* out, hipStream_t stream) {
   if (!time || !band || time->dim != band->dim) return ANCHA_HIP_INVALID;
-  const size_t rows = batch * bands * frames, dim = time->dim;
+  const size_t rows = batch * bands * frames;
   if (rows == 0) return ANCHA_HIP_OK;
   if (!x || !out || !time_rope || !band_rope || !workspace) return ANCHA_HIP_INVALID;
-  const size_t need = ancha_hip_axis_pair_workspace(time, band, rows);
-  if (workspace_bytes < need) return ANCHA_HIP_INVALID;
-  float* a = static_cast<float*>(workspace);
-  float* c = a + rows * dim;
-  void* inner = c + rows * dim;
-  const size_t inner_bytes = need - 2 * rows * dim * sizeof(float);
-  // Time pass: groups = batch * bands, sequence = frames.
-  int rc = ancha_hip_block_forward(time, x, batch * bands, frames, time_rope, inner, inner_bytes,
-                                   a, stream);
-  if (!rc) rc = ancha_hip_swap_axes(a, batch, bands, frames, dim, c, stream);
-  // Band pass: groups = batch * frames, sequence = bands.
-  if (!rc) rc = ancha_hip_block_forward(band, c, batch * frames, bands, band_rope, inner,
-                                        inner_bytes, a, stream);
-  if (!rc) rc = ancha_hip_swap_axes(a, batch, frames, bands, dim, out, stream);
+  if (workspace_bytes < ancha_hip_axis_pair_workspace(time, band, rows)) return ANCHA_HIP_INVALID;
+  // Time pass: groups = batch * bands, sequence = frames, x -> out.
+  int rc = block_forward(time, x, batch * bands, frames, 0, time_rope, workspace, workspace_bytes,
+                         out, stream);
+  // Band pass in place on the same [batch, bands, frames, dim] rows: groups = batch * frames,
+  // sequence = bands (network.rs:336-338 transposes instead).
+  if (!rc) rc = block_forward(band, out, batch * frames, bands, frames, band_rope, workspace,
+                              workspace_bytes, out, stream);
   return rc;
 }
 

@@ -223,7 +223,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
                              a.w * inv + bias.w);
       if (p.gelu) v = make_float4(gelu_erf(v.x), gelu_erf(v.y), gelu_erf(v.z), gelu_erf(v.w));
       if (rot) {
-        const int tok = (r0 + lrow) % p.tokens;
+        const int tok = ((r0 + lrow) / p.token_div) % p.tokens;
         const unsigned c = ((unsigned)(table * p.tokens + tok) * 64 + (col & 63)) * 4;
         v = rotate4(v, bload4<true>(roper, c), bload4<true>(roper, c + (unsigned)p.tokens * 256));
       }

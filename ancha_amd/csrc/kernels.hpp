@@ -6,7 +6,12 @@
 namespace ancha {
 
 // softmax(q.k^T).v per (group, head). q/k/v/gate point at the column of head 0 inside
-// [groups, tokens, ld*] row-major buffers (head h at +64h, group stride tokens*ld).
+// row-major buffers (head h at +64h). Token t of group g sits in row
+//   (g / gsplit) * gouter + (g % gsplit) * gstep + t * tstep
+// of q/k/v/gate (row stride ld*) and of out (row stride heads*64): gsplit 1, gouter tokens,
+// gstep 0, tstep 1 for groups of contiguous tokens ([groups, tokens, ...]); gsplit frames,
+// gouter bands*frames, gstep 1, tstep frames for the band axis of a [batch, bands, frames, ...]
+// buffer (group = batch*frames + frame, token = band). gsplit 0 means contiguous groups.
 struct AttnParams {
   const float* q;
   const float* k;
@@ -17,6 +22,8 @@ struct AttnParams {
   long ldq, ldk, ldv, ldg;
   int groups, tokens, heads;
   int out_half;       // store the output as fp16 (the block's internal activation)
+  int gsplit;
+  long gouter, gstep, tstep;
 };
 
 // `aligned`: every float4 access is 16-byte aligned (base pointers and row strides).
@@ -71,6 +78,7 @@ struct Gemm16Params {
   long ldx;
   int n, k, m;
   int tokens, width;
+  int token_div;  // rotary position of row r: (r / token_div) % tokens
   int gelu, norm, x_half, out_half;
 };
 

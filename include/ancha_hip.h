@@ -151,10 +151,12 @@ size_t ancha_hip_axis_pair_workspace(const ancha_hip_block *time, const ancha_hi
 
 /* One time pass + band pass of the RoFormer axis loop: x, out [batch, bands, frames, dim]
  * contiguous (out may alias x); the time block runs on groups = batch*bands with sequence
- * frames, the band block on groups = batch*frames with sequence bands (after an axis swap),
- * and the result is swapped back. time_rope [4, frames, 64], band_rope [4, bands, 64].
- * Allocates nothing. Replaces one iteration of the axis loop of the RoFormer networks
- * (network.rs:333-339). */
+ * frames, then the band block on groups = batch*frames with sequence bands, in place on the
+ * same rows: its attention reads each band sequence with a row stride of `frames` and its
+ * rotary epilogue takes the band index (row / frames) % bands, so no transposed copy is made.
+ * time_rope [4, frames, 64], band_rope [4, bands, 64]. Allocates nothing. Replaces one
+ * iteration of the axis loop of the RoFormer networks (network.rs:333-339), whose two dense
+ * `swap_dims` copies it removes. */
 int ancha_hip_axis_pair_forward(const ancha_hip_block *time, const ancha_hip_block *band,
                                 const float *x, size_t batch, size_t bands, size_t frames,
                                 const float *time_rope, const float *band_rope, void *workspace,
