@@ -47,6 +47,15 @@ SIGNATURES = {
     "ancha_hip_swap_axes": (_int, [_p, _sz, _sz, _sz, _sz, _p, _p]),
     "ancha_hip_axis_pair_workspace": (_sz, [_p, _p, _sz]),
     "ancha_hip_axis_pair_forward": (_int, [_p, _p, _p, _sz, _sz, _sz, _p, _p, _p, _sz, _p, _p]),
+    "ancha_hip_roformer_create": (_int, [_p, _p, _p, ctypes.POINTER(_p)]),
+    "ancha_hip_roformer_workspace": (_sz, [_p, _sz]),
+    "ancha_hip_roformer_forward": (_int, [_p, _p, _sz, _p, _sz, _p, _p]),
+    "ancha_hip_separate_workspace": (_sz, [_p, _sz]),
+    "ancha_hip_separate": (_int, [_p, _p, _sz, _p, _sz, _p, _p, _p]),
+    "ancha_hip_roformer_destroy": (None, [_p]),
+    "ancha_hip_stft": (_int, [_p, _sz, _sz, _p, _p]),
+    "ancha_hip_istft_workspace": (_sz, [_sz]),
+    "ancha_hip_istft": (_int, [_p, _p, _sz, _sz, _sz, _int, _p, _sz, _p, _p]),
     "ancha_hip_check": (_int, []),
     "ancha_hip_last_error": (ctypes.c_char_p, []),
 }

@@ -70,6 +70,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
   constexpr int xbytes = XH ? 2 : 4;
   const unsigned ldx_b = (unsigned)p.ldx * xbytes, k2 = (unsigned)k * 2;
   const int ktiles = (k + kBK - 1) / kBK;
+  const int batch_tiles = ((n + kBM - 1) / kBM) * col_tiles;  // tiles of one product
 
   // Tiles of this workgroup: XCD x (= blockIdx % 8) owns tiles [x*per, (x+1)*per); its
   // workgroups take every (gridDim/8)-th tile of that range.
@@ -88,11 +89,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
   // Loads K step t of tile `tile` (tile >= last: nothing; every load returns 0).
   auto load = [&](int tile, int t) {
     const bool live = tile < last;
-    const int r0 = live ? (tile / col_tiles) * kBM : 0, c0 = live ? (tile % col_tiles) * kBN : 0;
+    const int bt = live ? tile / batch_tiles : 0, rt = live ? tile % batch_tiles : 0;
+    const int r0 = live ? (rt / col_tiles) * kBM : 0, c0 = live ? (rt % col_tiles) * kBN : 0;
     const int rows = live ? min(kBM, n - r0) : 0;
-    const rsrc_t xr = make_rsrc(static_cast<const unsigned char*>(p.x) + (long)r0 * p.ldx * xbytes,
+    const rsrc_t xr = make_rsrc(static_cast<const unsigned char*>(p.x) +
+                                    (bt * p.x_bstride + (long)r0 * p.ldx) * xbytes,
                                 rows ? (unsigned)(((long)(rows - 1) * p.ldx + k) * xbytes) : 0u);
-    const rsrc_t wr = make_rsrc(p.wt + (long)c0 * k, live ? (unsigned)((long)kBN * k * 2) : 0u);
+    const rsrc_t wr = make_rsrc(p.wt + bt * p.w_bstride + (long)c0 * k,
+                                live ? (unsigned)((long)kBN * k * 2) : 0u);
     const int k0 = t * kBK;
     if constexpr (XH) {
       const int kc = k0 + 8 * c8;
@@ -160,14 +164,13 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
   // Epilogue constants: this thread's 4 output columns (c4) in the row-wise pass.
   const int c4 = tid & 31, erow = tid >> 5;
   const void* any = p.wt;  // base of the empty descriptors of absent operands
-  const rsrc_t biasr = make_rsrc(p.bias ? static_cast<const void*>(p.bias) : any,
-                                 p.bias ? (unsigned)m * 4 : 0u);
   const rsrc_t roper = make_rsrc(p.rope ? static_cast<const void*>(p.rope) : any,
                                  p.rope ? (unsigned)(4 * p.tokens * 64 * 4) : 0u);
 
   load(first, 0);
   for (int tile = first; tile < last; tile += slots) {
-    const int r0 = (tile / col_tiles) * kBM, c0 = (tile % col_tiles) * kBN;
+    const int bt = tile / batch_tiles, rt = tile % batch_tiles;
+    const int r0 = (rt / col_tiles) * kBM, c0 = (rt % col_tiles) * kBN;
     const int rows = min(kBM, n - r0);
     if constexpr (NORM)
       for (int i = 0; i < XP; i++) ss[i] = 0.f;
@@ -204,14 +207,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
 
     // Row-wise epilogue: bias -> GELU -> rotary -> residual (fused/gemm.rs:46-82 order).
     constexpr int obytes = OH ? 2 : 4;
-    const rsrc_t outr = make_rsrc(static_cast<unsigned char*>(p.out) + (long)r0 * m * obytes,
+    const long orow = bt * p.out_bstride + (long)r0 * m;
+    const rsrc_t outr = make_rsrc(static_cast<unsigned char*>(p.out) + orow * obytes,
                                   (unsigned)((long)rows * m * obytes));
-    const rsrc_t resr = make_rsrc(p.residual ? static_cast<const void*>(p.residual + (long)r0 * m)
-                                             : any,
+    const rsrc_t resr = make_rsrc(p.residual ? static_cast<const void*>(p.residual + orow) : any,
                                   p.residual ? (unsigned)((long)rows * m * 4) : 0u);
     const int col = c0 + 4 * c4;
     float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (p.bias) bias = bload4<true>(biasr, col * 4);
+    if (p.bias) bias = *reinterpret_cast<const float4*>(p.bias + bt * p.bias_bstride + col);
     const bool rot = p.rope && col < 2 * p.width;
     const int table = col < p.width ? 0 : 2;
     for (int i = 0; i < kBM / (NT / 32); i++) {
@@ -222,6 +225,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
       float4 v = make_float4(a.x * inv + bias.x, a.y * inv + bias.y, a.z * inv + bias.z,
                              a.w * inv + bias.w);
       if (p.gelu) v = make_float4(gelu_erf(v.x), gelu_erf(v.y), gelu_erf(v.z), gelu_erf(v.w));
+      if (p.tanh_act) v = make_float4(tanhf(v.x), tanhf(v.y), tanhf(v.z), tanhf(v.w));
       if (rot) {
         const int tok = ((r0 + lrow) / p.token_div) % p.tokens;
         const unsigned c = ((unsigned)(table * p.tokens + tok) * 64 + (col & 63)) * 4;
@@ -269,7 +273,7 @@ int device_cus() {
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream) {
   const int row_tiles = (p.n + kBM - 1) / kBM, col_tiles = p.m / kBN;
-  const int tiles = row_tiles * col_tiles;
+  const int tiles = row_tiles * col_tiles * (p.batch > 1 ? p.batch : 1);
   // Resident workgroups only (two 4-wave ones per CU for fp16 x; one 8-wave one for fp32 x,
   // whose registers allow three waves per SIMD), a multiple of the XCD count, no more than the
   // tiles need.

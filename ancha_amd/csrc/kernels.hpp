@@ -80,9 +80,64 @@ struct Gemm16Params {
   int tokens, width;
   int token_div;  // rotary position of row r: (r / token_div) % tokens
   int gelu, norm, x_half, out_half;
+  int tanh_act;   // tanh after the bias (the mask estimator's hidden layers)
+  // Batched products (batch > 1): product b reads x + b*x_bstride, wt + b*w_bstride,
+  // bias + b*bias_bstride and writes out (and reads residual) at + b*out_bstride (elements).
+  // Rotary epilogues are for unbatched calls.
+  int batch;
+  long x_bstride, w_bstride, bias_bstride, out_bstride;
 };
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream);
+
+// Separation runtime (dsp.hip), n_fft = 2048. chunk / audio [2][samples]; spectrum
+// [frames][1025][channel][re, im]; masks [2050][re, im][frames] (one stem); frames_buf
+// [frames][2][2048]; sums [2][total], weights [total].
+hipError_t launch_stft(const float* chunk, long samples, int hop, float* spectrum,
+                       hipStream_t stream);
+hipError_t launch_istft_frames(const float* spectrum, const float* masks, int frames, int zero_dc,
+                               float* frames_buf, hipStream_t stream);
+hipError_t launch_ola_accumulate(const float* frames_buf, int frames, int hop, long length,
+                                 long start, long total, bool first, bool last, bool count_weight,
+                                 float* sums, float* weights, hipStream_t stream);
+hipError_t launch_chunk_gather(const float* audio, long n, long start, long border,
+                               long remaining, long samples, float* chunk, hipStream_t stream);
+hipError_t launch_finish(const float* sums, const float* weights, long total, long border, long n,
+                         const float* audio, float* out, float* residual, hipStream_t stream);
+hipError_t launch_zero(float* p, long n, hipStream_t stream);
+
+// Band split (mel.hip): spectrum [frames][cols]; band b = FFT bins bins[offsets[b] ..
+// offsets[b+1]), feature columns 4*bin .. 4*bin+3; weight: per band [width][dim] fp32 (folded
+// scale applied) starting at element wofs[b] * dim; bias [bands][dim]; x [bands][frames][dim].
+struct BandSplitParams {
+  const float* spectrum;
+  const int* offsets;
+  const int* bins;
+  const int* wofs;
+  const float* weight;
+  const float* bias;
+  float* x;
+  int bands, frames, cols, dim, max_width;
+  int tile;  // frames per workgroup (set by the launcher)
+};
+hipError_t launch_band_split(const BandSplitParams& p, hipStream_t stream);
+
+// GLU masks (mel.hip): glu holds, per band b at band_base[b] * frames, [frames][band_stride[b]] fp32
+// rows whose first band_width[b] columns are the values and next band_width[b] the gates.
+// FFT bin f is covered by entries cover_start[f] .. cover_start[f+1] (band, local bin).
+// masks [outputs = 4 * bins][frames] with output 4f + 2*channel + re/im.
+struct GluParams {
+  const float* glu;
+  const long* band_base;
+  const int* band_stride;
+  const int* band_width;
+  const int* cover_start;
+  const int* cover_band;
+  const int* cover_local;
+  float* masks;
+  int outputs, frames;
+};
+hipError_t launch_glu_gather(const GluParams& p, hipStream_t stream);
 
 // out [batch, b, a, dim] = x [batch, a, b, dim] with axes 1 and 2 swapped (both contiguous).
 struct SwapParams {

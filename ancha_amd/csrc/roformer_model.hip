@@ -1,0 +1,640 @@
+// The Mel/BS-RoFormer network and the chunked separation runtime on the gfx950 kernels (C ABI
+// of include/ancha_hip.h), host code only.
+//
+// Mirrors crates/ancha-models/src/network.rs (Roformer::build :89-278, forward :303-400) and
+// the chunk loop of src/runtime.rs:103-238:
+//   spectrum -> band split (mel.hip) -> depth x [time block, frequency block] (block.hip, the
+//   frequency block reading the time layout in place) -> [BS: final norm] -> per stem: tanh
+//   hidden layers and the value|gate output projection as batched fp16 GEMMs (gemm16.hip),
+//   GLU + overlap gather (mel.hip) -> masks [stems][2*bins][re, im][frames].
+//   separate: per chunk gather -> STFT -> forward -> per stem masked iSTFT + overlap-add into
+//   the clip accumulators (dsp.hip); finally the accumulator division and border crop.
+// Weights come from a callback that serves the reference checkpoint's tensors by name.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/ancha_hip.h"
+#include "kernels.hpp"
+
+namespace {
+
+constexpr size_t kFft = 2048;
+constexpr size_t kHeadDim = ANCHA_ATTENTION_HEAD_DIM;
+
+size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+template <typename T>
+int upload(const std::vector<T>& host, T** dev) {
+  *dev = nullptr;
+  if (host.empty()) return 0;
+  hipError_t e = hipMalloc(reinterpret_cast<void**>(dev), host.size() * sizeof(T));
+  if (e == hipSuccess)
+    e = hipMemcpy(*dev, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice);
+  return e == hipSuccess ? 0 : -static_cast<int>(e);
+}
+
+// AxisRope::new (roformer.rs:282-302): [4][tokens][64] = query cos, query signed sin (both
+// times 1/sqrt(64)), key cos, key signed sin; angle = f32(t) * f.
+std::vector<float> axis_rope(const std::vector<float>& freqs, size_t tokens) {
+  const size_t nf = freqs.size(), width = 2 * nf;
+  const float scale = 1.0f / std::sqrt(static_cast<float>(width));
+  std::vector<float> out(4 * tokens * width);
+  size_t p = 0;
+  for (int table = 0; table < 2; table++) {
+    const float s_ = table == 0 ? scale : 1.0f;
+    for (int sine = 0; sine < 2; sine++)
+      for (size_t t = 0; t < tokens; t++)
+        for (size_t i = 0; i < nf; i++) {
+          const float angle = static_cast<float>(t) * freqs[i];
+          const float s = std::sin(angle), c = std::cos(angle);
+          out[p++] = sine ? -s * s_ : c * s_;
+          out[p++] = sine ? s * s_ : c * s_;
+        }
+  }
+  return out;
+}
+
+}  // namespace
+
+struct ancha_hip_roformer {
+  bool mel, zero_dc;
+  size_t dim, depth, heads, ff_hidden, mask_hidden, mask_layers, hop, chunk, overlap, stems;
+  size_t bands, fft_bins, max_width;
+  std::vector<size_t> offsets, bins, widths, wofs;
+  int device;
+  int *d_offsets = nullptr, *d_bins = nullptr, *d_wofs = nullptr;
+  float *split_w = nullptr, *split_b = nullptr;
+  std::vector<ancha_hip_block*> blocks;  // time, frequency per depth
+  std::vector<std::vector<float>> freqs;
+  float* final_scale = nullptr;
+  struct Head {
+    std::vector<_Float16*> hw;
+    std::vector<float*> hb;
+    _Float16* ow = nullptr;
+    float* ob = nullptr;
+  };
+  std::vector<Head> mask_heads;
+  struct Class {
+    size_t b0, b1, m_pad;
+  };
+  std::vector<Class> classes;
+  std::vector<size_t> mpad, colprefix;  // per band padded output width, prefix (columns)
+  long* d_band_base = nullptr;
+  int *d_band_stride = nullptr, *d_band_width = nullptr;
+  int *d_cover_start = nullptr, *d_cover_band = nullptr, *d_cover_local = nullptr;
+  // Rotary tables [4][tokens][64] per block, for the frame count they were built for.
+  size_t rope_frames = 0;
+  std::vector<float*> time_rope, band_rope;
+};
+
+namespace {
+
+void free_all(ancha_hip_roformer* m) {
+  if (!m) return;
+  for (void* p : {static_cast<void*>(m->d_offsets), static_cast<void*>(m->d_bins),
+                  static_cast<void*>(m->d_wofs), static_cast<void*>(m->split_w),
+                  static_cast<void*>(m->split_b), static_cast<void*>(m->final_scale),
+                  static_cast<void*>(m->d_band_base), static_cast<void*>(m->d_band_stride),
+                  static_cast<void*>(m->d_band_width), static_cast<void*>(m->d_cover_start),
+                  static_cast<void*>(m->d_cover_band), static_cast<void*>(m->d_cover_local)})
+    if (p) (void)hipFree(p);
+  for (auto* b : m->blocks) ancha_hip_block_destroy(b);
+  for (auto& h : m->mask_heads) {
+    for (auto* p : h.hw) (void)hipFree(p);
+    for (auto* p : h.hb) (void)hipFree(p);
+    if (h.ow) (void)hipFree(h.ow);
+    if (h.ob) (void)hipFree(h.ob);
+  }
+  for (auto* p : m->time_rope) (void)hipFree(p);
+  for (auto* p : m->band_rope) (void)hipFree(p);
+  delete m;
+}
+
+// One (batched) product through the block GEMM: out = act(x . W^T + bias).
+int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, size_t m,
+         const float* bias, bool tanh_act, void* out, bool out_half, size_t batch,
+         long x_bstride, long w_bstride, long bias_bstride, long out_bstride,
+         hipStream_t stream) {
+  ancha::Gemm16Params p{};
+  p.x = x;
+  p.wt = wt;
+  p.bias = bias;
+  p.out = out;
+  p.ldx = static_cast<long>(k);
+  p.n = static_cast<int>(n);
+  p.k = static_cast<int>(k);
+  p.m = static_cast<int>(m);
+  p.tokens = 1;
+  p.token_div = 1;
+  p.x_half = x_half;
+  p.out_half = out_half;
+  p.tanh_act = tanh_act;
+  p.batch = static_cast<int>(batch);
+  p.x_bstride = x_bstride;
+  p.w_bstride = w_bstride;
+  p.bias_bstride = bias_bstride;
+  p.out_bstride = out_bstride;
+  const hipError_t e = ancha::launch_gemm16(p, stream);
+  return e == hipSuccess ? 0 : -static_cast<int>(e);
+}
+
+// Rotary tables for `frames` time steps (built on first use of a frame count).
+int ensure_rope(ancha_hip_roformer* m, size_t frames) {
+  if (m->rope_frames == frames) return 0;
+  for (auto* p : m->time_rope) (void)hipFree(p);
+  for (auto* p : m->band_rope) (void)hipFree(p);
+  m->time_rope.assign(m->depth, nullptr);
+  m->band_rope.assign(m->depth, nullptr);
+  m->rope_frames = 0;
+  for (size_t i = 0; i < m->depth; i++) {
+    int rc = upload(axis_rope(m->freqs[2 * i], frames), &m->time_rope[i]);
+    if (!rc) rc = upload(axis_rope(m->freqs[2 * i + 1], m->bands), &m->band_rope[i]);
+    if (rc) return rc;
+  }
+  m->rope_frames = frames;
+  return 0;
+}
+
+// Workspace regions of a forward over `frames` frames.
+struct Layout {
+  size_t x, inner, h1, h2, glu, total;
+};
+Layout forward_layout(const ancha_hip_roformer* m, size_t frames) {
+  Layout l{};
+  const size_t rows = m->bands * frames;
+  l.x = 0;
+  const size_t block_ws =
+      ancha_hip_axis_pair_workspace(m->blocks[0], m->blocks[1], rows);
+  l.inner = round_up(rows * m->dim * 4, 256);
+  l.h1 = l.inner;
+  l.h2 = l.h1 + round_up(rows * m->mask_hidden * 2, 256);
+  l.glu = l.h2 + round_up(rows * m->mask_hidden * 2, 256);
+  const size_t heads_end = l.glu + round_up(frames * m->colprefix.back() * 4, 256);
+  const size_t blocks_end = l.inner + round_up(block_ws, 256);
+  l.total = heads_end > blocks_end ? heads_end : blocks_end;
+  return l;
+}
+
+int forward_impl(ancha_hip_roformer* m, const float* spectrum, size_t frames, void* workspace,
+                 float* masks, hipStream_t stream) {
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  const Layout l = forward_layout(m, frames);
+  float* x = reinterpret_cast<float*>(ws + l.x);
+  const size_t rows = m->bands * frames;
+  int rc = ensure_rope(m, frames);
+  if (rc) return rc;
+  ancha::BandSplitParams bp{};
+  bp.spectrum = spectrum;
+  bp.offsets = m->d_offsets;
+  bp.bins = m->d_bins;
+  bp.wofs = m->d_wofs;
+  bp.weight = m->split_w;
+  bp.bias = m->split_b;
+  bp.x = x;
+  bp.bands = static_cast<int>(m->bands);
+  bp.frames = static_cast<int>(frames);
+  bp.cols = static_cast<int>(4 * m->fft_bins);
+  bp.dim = static_cast<int>(m->dim);
+  bp.max_width = static_cast<int>(m->max_width);
+  hipError_t e = ancha::launch_band_split(bp, stream);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  // Axis loop (network.rs:333-339): x [bands][frames][dim] is the time layout with batch 1.
+  const size_t block_bytes = l.total - l.inner;
+  for (size_t i = 0; i < m->depth; i++) {
+    rc = ancha_hip_axis_pair_forward(m->blocks[2 * i], m->blocks[2 * i + 1], x, 1, m->bands,
+                                     frames, m->time_rope[i], m->band_rope[i], ws + l.inner,
+                                     block_bytes, x, stream);
+    if (rc) return rc;
+  }
+  if (m->final_scale) {
+    rc = ancha_hip_unit_norm(x, rows, m->dim, m->dim, m->final_scale, x, stream);
+    if (rc) return rc;
+  }
+  _Float16* h[2] = {reinterpret_cast<_Float16*>(ws + l.h1), reinterpret_cast<_Float16*>(ws + l.h2)};
+  float* glu = reinterpret_cast<float*>(ws + l.glu);
+  const size_t mh = m->mask_hidden;
+  for (size_t s = 0; s < m->stems; s++) {
+    const ancha_hip_roformer::Head& head = m->mask_heads[s];
+    // Hidden layers (network.rs:377-379): h = tanh(W h + b) per band, fp16 between layers.
+    const void* in = x;
+    bool in_half = false;
+    size_t in_dim = m->dim;
+    for (size_t layer = 0; layer < m->mask_layers; layer++) {
+      _Float16* out = h[layer & 1];
+      rc = gemm(in, in_half, frames, in_dim, head.hw[layer], mh, head.hb[layer], true, out, true,
+                m->bands, static_cast<long>(frames * in_dim), static_cast<long>(mh * in_dim),
+                static_cast<long>(mh), static_cast<long>(frames * mh), stream);
+      if (rc) return rc;
+      in = out;
+      in_half = true;
+      in_dim = mh;
+    }
+    // Output projection, value and gate halves side by side, one batched product per run of
+    // bands with the same padded width.
+    for (const auto& c : m->classes) {
+      rc = gemm(static_cast<const _Float16*>(in) + c.b0 * frames * mh, true, frames, mh,
+                head.ow + m->colprefix[c.b0] * mh, c.m_pad, head.ob + m->colprefix[c.b0], false,
+                glu + m->colprefix[c.b0] * frames, false, c.b1 - c.b0,
+                static_cast<long>(frames * mh), static_cast<long>(c.m_pad * mh),
+                static_cast<long>(c.m_pad), static_cast<long>(frames * c.m_pad), stream);
+      if (rc) return rc;
+    }
+    ancha::GluParams gp{};
+    gp.glu = glu;
+    gp.band_base = m->d_band_base;
+    gp.band_stride = m->d_band_stride;
+    gp.band_width = m->d_band_width;
+    gp.cover_start = m->d_cover_start;
+    gp.cover_band = m->d_cover_band;
+    gp.cover_local = m->d_cover_local;
+    gp.masks = masks + s * 4 * m->fft_bins * frames;
+    gp.outputs = static_cast<int>(4 * m->fft_bins);
+    gp.frames = static_cast<int>(frames);
+    e = ancha::launch_glu_gather(gp, stream);
+    if (e != hipSuccess) return -static_cast<int>(e);
+  }
+  return 0;
+}
+
+// Chunk plan of src/runtime.rs:103-116 and ChunkPlan (chunk.rs:1-25).
+struct Plan {
+  size_t step, border, length, frames;
+  std::vector<size_t> starts;
+};
+Plan plan_for(const ancha_hip_roformer* m, size_t samples) {
+  Plan p{};
+  p.step = m->chunk / m->overlap;
+  p.border = m->chunk - p.step;
+  if (!(samples > 2 * p.border)) p.border = 0;
+  p.length = samples + 2 * p.border;
+  for (size_t s = 0; s < p.length; s += p.step) p.starts.push_back(s);
+  p.frames = m->chunk / m->hop + 1;
+  return p;
+}
+
+struct SepLayout {
+  size_t chunk, spectrum, masks, frames_buf, sums, weights, model, total;
+};
+SepLayout separate_layout(const ancha_hip_roformer* m, size_t samples) {
+  const Plan p = plan_for(m, samples);
+  SepLayout l{};
+  size_t o = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = o;
+    o += round_up(bytes, 256);
+    return at;
+  };
+  l.chunk = take(2 * m->chunk * 4);
+  l.spectrum = take(p.frames * 4 * m->fft_bins * 4);
+  l.masks = take(m->stems * 4 * m->fft_bins * p.frames * 4);
+  l.frames_buf = take(p.frames * 2 * kFft * 4);
+  l.sums = take(m->stems * 2 * p.length * 4);
+  l.weights = take(p.length * 4);
+  l.model = take(forward_layout(m, p.frames).total);
+  l.total = o;
+  return l;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+extern "C" {
+
+int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tensor_fn get,
+                              void* ctx, ancha_hip_roformer** model) {
+  if (!model) return ANCHA_HIP_INVALID;
+  *model = nullptr;
+  if (!c || !get || !c->band_offsets || !c->band_bins) return ANCHA_HIP_INVALID;
+  if (!ancha_hip_available()) return ANCHA_HIP_UNSUPPORTED;
+  // Schema checks (config.rs:36-121) plus what the kernels cover.
+  if (c->n_fft != kFft || c->head_dim != kHeadDim || c->hop == 0 || c->hop > kFft / 2 ||
+      c->dim == 0 || c->depth == 0 || c->heads == 0 || c->ff_mult == 0 || c->mask_depth == 0 ||
+      c->mask_expansion == 0 || c->stems == 0 || c->stems > 2 || c->bands < 2 ||
+      c->chunk_samples <= kFft / 2 || c->overlap == 0 || c->overlap > c->chunk_samples ||
+      (!c->mel && c->mask_depth < 2))
+    return ANCHA_HIP_INVALID;
+  const size_t fft_bins = kFft / 2 + 1;
+  std::vector<int> coverage(fft_bins, 0);
+  for (size_t b = 0; b < c->bands; b++) {
+    if (c->band_offsets[b + 1] <= c->band_offsets[b]) return ANCHA_HIP_INVALID;
+    for (size_t q = c->band_offsets[b]; q < c->band_offsets[b + 1]; q++) {
+      if (c->band_bins[q] >= fft_bins) return ANCHA_HIP_INVALID;
+      if (q > c->band_offsets[b] && c->band_bins[q] <= c->band_bins[q - 1])
+        return ANCHA_HIP_INVALID;
+      coverage[c->band_bins[q]]++;
+    }
+  }
+  for (int n : coverage)
+    if (n == 0) return ANCHA_HIP_INVALID;  // "bands leave uncovered FFT bins"
+  const size_t dim = c->dim, mh = c->dim * c->mask_expansion;
+  if (!ancha_hip_linear_supported(dim, mh) || !ancha_hip_linear_supported(mh, mh))
+    return ANCHA_HIP_UNSUPPORTED;
+
+  auto* m = new (std::nothrow) ancha_hip_roformer{};
+  if (!m) return ANCHA_HIP_INVALID;
+  m->mel = c->mel != 0;
+  m->zero_dc = c->zero_dc != 0;
+  m->dim = dim;
+  m->depth = c->depth;
+  m->heads = c->heads;
+  m->ff_hidden = dim * c->ff_mult;
+  m->mask_hidden = mh;
+  // BS depth counts all Linears, Mel depth counts hidden layers (network.rs:138-144).
+  m->mask_layers = m->mel ? c->mask_depth : c->mask_depth - 1;
+  m->hop = c->hop;
+  m->chunk = c->chunk_samples;
+  m->overlap = c->overlap;
+  m->stems = c->stems;
+  m->bands = c->bands;
+  m->fft_bins = fft_bins;
+  if (hipGetDevice(&m->device) != hipSuccess) m->device = 0;
+  m->offsets.assign(c->band_offsets, c->band_offsets + c->bands + 1);
+  m->bins.assign(c->band_bins, c->band_bins + m->offsets.back());
+  m->wofs.assign(c->bands + 1, 0);
+  m->max_width = 0;
+  for (size_t b = 0; b < c->bands; b++) {
+    const size_t w = 4 * (m->offsets[b + 1] - m->offsets[b]);
+    m->widths.push_back(w);
+    m->wofs[b + 1] = m->wofs[b] + w;
+    if (w > m->max_width) m->max_width = w;
+  }
+  int rc = 0;
+  auto fail = [&](int code) {
+    free_all(m);
+    return code;
+  };
+  auto tensor = [&](const std::string& name, size_t numel) -> const float* {
+    return get(ctx, name.c_str(), numel);
+  };
+  // Band split (network.rs:96-121): W'[c][d] = W[d][c] * sqrt(width) * gamma[c], [width][dim].
+  {
+    std::vector<float> w(m->wofs.back() * dim), bias(c->bands * dim);
+    for (size_t b = 0; b < c->bands; b++) {
+      const size_t width = m->widths[b];
+      const std::string p = "band_split.to_features." + std::to_string(b);
+      const float* g = tensor(p + ".0.gamma", width);
+      const float* wt = tensor(p + ".1.weight", dim * width);
+      const float* bs = tensor(p + ".1.bias", dim);
+      if (!g || !wt || !bs) return fail(ANCHA_HIP_INVALID);
+      const float root = std::sqrt(static_cast<float>(width));
+      for (size_t d = 0; d < dim; d++)
+        for (size_t col = 0; col < width; col++)
+          w[(m->wofs[b] + col) * dim + d] = wt[d * width + col] * (g[col] * root);
+      for (size_t d = 0; d < dim; d++) bias[b * dim + d] = bs[d];
+    }
+    std::vector<int> off(m->offsets.begin(), m->offsets.end()), bins(m->bins.begin(), m->bins.end());
+    std::vector<int> wofs(m->wofs.begin(), m->wofs.end());
+    if (!rc) rc = upload(w, &m->split_w);
+    if (!rc) rc = upload(bias, &m->split_b);
+    if (!rc) rc = upload(off, &m->d_offsets);
+    if (!rc) rc = upload(bins, &m->d_bins);
+    if (!rc) rc = upload(wofs, &m->d_wofs);
+    if (rc) return fail(rc);
+  }
+  // Transformer blocks (network.rs:122-137; Transformer::load, roformer.rs:381-409).
+  for (size_t i = 0; i < c->depth; i++)
+    for (int axis = 0; axis < 2; axis++) {
+      const std::string p = "layers." + std::to_string(i) + "." + std::to_string(axis);
+      const size_t inner = c->heads * kHeadDim, hidden = m->ff_hidden;
+      const std::string a = p + ".layers.0.0", f = p + ".layers.0.1.net";
+      const float* t[11] = {
+          tensor(a + ".norm.gamma", dim),         tensor(a + ".to_qkv.weight", 3 * inner * dim),
+          tensor(a + ".to_gates.weight", c->heads * dim), tensor(a + ".to_gates.bias", c->heads),
+          tensor(a + ".to_out.0.weight", dim * inner),    tensor(f + ".0.gamma", dim),
+          tensor(f + ".1.weight", hidden * dim),          tensor(f + ".1.bias", hidden),
+          tensor(f + ".4.weight", dim * hidden),          tensor(f + ".4.bias", dim),
+          m->mel ? tensor(p + ".norm.gamma", dim) : nullptr};
+      const float* fr = tensor(a + ".rotary_embed.freqs", kHeadDim / 2);
+      for (int j = 0; j < 10; j++)
+        if (!t[j]) return fail(ANCHA_HIP_INVALID);
+      if (!fr || (m->mel && !t[10])) return fail(ANCHA_HIP_INVALID);
+      ancha_hip_block* blk = nullptr;
+      rc = ancha_hip_block_create(dim, c->heads, hidden, t[0], t[1], t[2], t[3], t[4], t[5], t[6],
+                                  t[7], t[8], t[9], t[10], &blk);
+      if (rc) return fail(rc);
+      m->blocks.push_back(blk);
+      m->freqs.emplace_back(fr, fr + kHeadDim / 2);
+    }
+  if (!m->mel) {  // final_norm (network.rs:138-142, :340-342)
+    const float* g = tensor("final_norm.gamma", dim);
+    if (!g) return fail(ANCHA_HIP_INVALID);
+    std::vector<float> s(dim);
+    const float root = std::sqrt(static_cast<float>(dim));
+    for (size_t d = 0; d < dim; d++) s[d] = g[d] * root;
+    rc = upload(s, &m->final_scale);
+    if (rc) return fail(rc);
+  }
+  // Output classes: runs of bands whose value|gate width pads to the same multiple of 128.
+  m->mpad.resize(c->bands);
+  m->colprefix.assign(c->bands + 1, 0);
+  for (size_t b = 0; b < c->bands; b++) {
+    m->mpad[b] = round_up(2 * m->widths[b], 128);
+    m->colprefix[b + 1] = m->colprefix[b] + m->mpad[b];
+    if (b == 0 || m->mpad[b] != m->classes.back().m_pad)
+      m->classes.push_back({b, b + 1, m->mpad[b]});
+    else
+      m->classes.back().b1 = b + 1;
+  }
+  // Mask heads (network.rs:143-177): hidden layers [bands][out][in] fp16, output [m_pad][mh].
+  for (size_t s = 0; s < c->stems; s++) {
+    ancha_hip_roformer::Head head;
+    m->mask_heads.push_back(head);
+    ancha_hip_roformer::Head& h = m->mask_heads.back();
+    auto key = [&](size_t b, size_t layer) {
+      return "mask_estimators." + std::to_string(s) + ".to_freqs." + std::to_string(b) + ".0." +
+             std::to_string(2 * layer);
+    };
+    size_t in = dim;
+    for (size_t layer = 0; layer < m->mask_layers; layer++) {
+      std::vector<_Float16> w(c->bands * mh * in);
+      std::vector<float> bias(c->bands * mh);
+      for (size_t b = 0; b < c->bands; b++) {
+        const float* wt = tensor(key(b, layer) + ".weight", mh * in);
+        const float* bs = tensor(key(b, layer) + ".bias", mh);
+        if (!wt || !bs) return fail(ANCHA_HIP_INVALID);
+        for (size_t e = 0; e < mh * in; e++) w[b * mh * in + e] = static_cast<_Float16>(wt[e]);
+        for (size_t o = 0; o < mh; o++) bias[b * mh + o] = bs[o];
+      }
+      _Float16* dw = nullptr;
+      float* db = nullptr;
+      rc = upload(w, &dw);
+      h.hw.push_back(dw);
+      if (!rc) rc = upload(bias, &db);
+      h.hb.push_back(db);
+      if (rc) return fail(rc);
+      in = mh;
+    }
+    std::vector<_Float16> ow(m->colprefix.back() * mh, static_cast<_Float16>(0.0f));
+    std::vector<float> ob(m->colprefix.back(), 0.0f);
+    for (size_t b = 0; b < c->bands; b++) {
+      const size_t w2 = 2 * m->widths[b];
+      const float* wt = tensor(key(b, m->mask_layers) + ".weight", w2 * mh);
+      const float* bs = tensor(key(b, m->mask_layers) + ".bias", w2);
+      if (!wt || !bs) return fail(ANCHA_HIP_INVALID);
+      for (size_t r = 0; r < w2; r++) {
+        for (size_t e = 0; e < mh; e++)
+          ow[(m->colprefix[b] + r) * mh + e] = static_cast<_Float16>(wt[r * mh + e]);
+        ob[m->colprefix[b] + r] = bs[r];
+      }
+    }
+    rc = upload(ow, &h.ow);
+    if (!rc) rc = upload(ob, &h.ob);
+    if (rc) return fail(rc);
+  }
+  // GLU gather tables (network.rs:248-263): covering (band, local bin) entries per FFT bin.
+  {
+    std::vector<std::vector<std::pair<int, int>>> cover(fft_bins);
+    for (size_t b = 0; b < c->bands; b++)
+      for (size_t q = m->offsets[b]; q < m->offsets[b + 1]; q++)
+        cover[m->bins[q]].push_back({static_cast<int>(b), static_cast<int>(q - m->offsets[b])});
+    std::vector<int> start(fft_bins + 1, 0), band, local;
+    for (size_t f = 0; f < fft_bins; f++) {
+      for (auto& e : cover[f]) {
+        band.push_back(e.first);
+        local.push_back(e.second);
+      }
+      start[f + 1] = static_cast<int>(band.size());
+    }
+    std::vector<long> base(c->bands);
+    std::vector<int> stride(c->bands), width(c->bands);
+    for (size_t b = 0; b < c->bands; b++) {
+      base[b] = static_cast<long>(m->colprefix[b]);
+      stride[b] = static_cast<int>(m->mpad[b]);
+      width[b] = static_cast<int>(m->widths[b]);
+    }
+    rc = upload(start, &m->d_cover_start);
+    if (!rc) rc = upload(band, &m->d_cover_band);
+    if (!rc) rc = upload(local, &m->d_cover_local);
+    if (!rc) rc = upload(base, &m->d_band_base);
+    if (!rc) rc = upload(stride, &m->d_band_stride);
+    if (!rc) rc = upload(width, &m->d_band_width);
+    if (rc) return fail(rc);
+  }
+  rc = ensure_rope(m, c->chunk_samples / c->hop + 1);
+  if (rc) return fail(rc);
+  *model = m;
+  return ANCHA_HIP_OK;
+}
+
+size_t ancha_hip_roformer_workspace(const ancha_hip_roformer* m, size_t frames) {
+  if (!m || frames == 0) return 0;
+  return forward_layout(m, frames).total;
+}
+
+int ancha_hip_roformer_forward(ancha_hip_roformer* m, const float* spectrum, size_t frames,
+                               void* workspace, size_t workspace_bytes, float* masks,
+                               hipStream_t stream) {
+  if (!m) return ANCHA_HIP_INVALID;
+  if (frames == 0) return ANCHA_HIP_OK;
+  if (!spectrum || !workspace || !masks || !aligned16(spectrum) || !aligned16(workspace) ||
+      !aligned16(masks))
+    return ANCHA_HIP_INVALID;
+  if (workspace_bytes < ancha_hip_roformer_workspace(m, frames)) return ANCHA_HIP_INVALID;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev != m->device) return ANCHA_HIP_INVALID;
+  return forward_impl(m, spectrum, frames, workspace, masks, stream);
+}
+
+size_t ancha_hip_separate_workspace(const ancha_hip_roformer* m, size_t samples) {
+  if (!m || samples == 0) return 0;
+  return separate_layout(m, samples).total;
+}
+
+int ancha_hip_separate(ancha_hip_roformer* m, const float* audio, size_t samples, void* workspace,
+                       size_t workspace_bytes, float* stems, float* residual,
+                       hipStream_t stream) {
+  if (!m) return ANCHA_HIP_INVALID;
+  if (samples == 0) return ANCHA_HIP_OK;
+  if (!audio || !workspace || !stems || !aligned16(workspace)) return ANCHA_HIP_INVALID;
+  if (residual && m->stems != 1) return ANCHA_HIP_INVALID;
+  if (workspace_bytes < ancha_hip_separate_workspace(m, samples)) return ANCHA_HIP_INVALID;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev != m->device) return ANCHA_HIP_INVALID;
+  const Plan p = plan_for(m, samples);
+  const SepLayout l = separate_layout(m, samples);
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  float* chunk = reinterpret_cast<float*>(ws + l.chunk);
+  float* spectrum = reinterpret_cast<float*>(ws + l.spectrum);
+  float* masks = reinterpret_cast<float*>(ws + l.masks);
+  float* frames_buf = reinterpret_cast<float*>(ws + l.frames_buf);
+  float* sums = reinterpret_cast<float*>(ws + l.sums);
+  float* weights = reinterpret_cast<float*>(ws + l.weights);
+  const long length = static_cast<long>(p.length), cs = static_cast<long>(m->chunk);
+  hipError_t e = ancha::launch_zero(sums, static_cast<long>(m->stems) * 2 * length, stream);
+  if (e == hipSuccess) e = ancha::launch_zero(weights, length, stream);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  const size_t mask_stride = 4 * m->fft_bins * p.frames;
+  for (size_t start : p.starts) {
+    const long remaining = std::min<long>(length - static_cast<long>(start), cs);
+    e = ancha::launch_chunk_gather(audio, static_cast<long>(samples), static_cast<long>(start),
+                                   static_cast<long>(p.border), remaining, cs, chunk, stream);
+    if (e == hipSuccess) e = ancha::launch_stft(chunk, cs, static_cast<int>(m->hop), spectrum, stream);
+    if (e != hipSuccess) return -static_cast<int>(e);
+    int rc = forward_impl(m, spectrum, p.frames, ws + l.model, masks, stream);
+    if (rc) return rc;
+    const bool first = start == 0, last = static_cast<long>(start) + cs >= length;
+    for (size_t s = 0; s < m->stems; s++) {
+      e = ancha::launch_istft_frames(spectrum, masks + s * mask_stride, static_cast<int>(p.frames),
+                                     m->zero_dc ? 1 : 0, frames_buf, stream);
+      if (e == hipSuccess)
+        e = ancha::launch_ola_accumulate(frames_buf, static_cast<int>(p.frames),
+                                         static_cast<int>(m->hop), cs, static_cast<long>(start),
+                                         length, first, last, s == 0, sums + s * 2 * length,
+                                         weights, stream);
+      if (e != hipSuccess) return -static_cast<int>(e);
+    }
+  }
+  for (size_t s = 0; s < m->stems; s++) {
+    e = ancha::launch_finish(sums + s * 2 * length, weights, length, static_cast<long>(p.border),
+                             static_cast<long>(samples), audio, stems + s * 2 * samples,
+                             s == 0 ? residual : nullptr, stream);
+    if (e != hipSuccess) return -static_cast<int>(e);
+  }
+  return ANCHA_HIP_OK;
+}
+
+void ancha_hip_roformer_destroy(ancha_hip_roformer* m) { free_all(m); }
+
+int ancha_hip_stft(const float* signal, size_t samples, size_t hop, float* spectrum,
+                   hipStream_t stream) {
+  if (samples == 0) return ANCHA_HIP_OK;
+  if (!signal || !spectrum || hop == 0 || hop > kFft / 2 || samples <= kFft / 2 ||
+      !aligned16(spectrum))
+    return ANCHA_HIP_INVALID;
+  if (samples / hop + 1 > 0x7fffffff) return ANCHA_HIP_UNSUPPORTED;
+  const hipError_t e = ancha::launch_stft(signal, static_cast<long>(samples),
+                                          static_cast<int>(hop), spectrum, stream);
+  return e == hipSuccess ? 0 : -static_cast<int>(e);
+}
+
+size_t ancha_hip_istft_workspace(size_t frames) { return frames * 2 * kFft * sizeof(float); }
+
+int ancha_hip_istft(const float* spectrum, const float* masks, size_t frames, size_t hop,
+                    size_t length, int zero_dc, void* workspace, size_t workspace_bytes,
+                    float* out, hipStream_t stream) {
+  if (frames == 0 || length == 0) return ANCHA_HIP_OK;
+  if (!spectrum || !masks || !workspace || !out || hop == 0 || hop > kFft / 2)
+    return ANCHA_HIP_INVALID;
+  if (length + kFft / 2 > (frames - 1) * hop + kFft) return ANCHA_HIP_INVALID;
+  if (workspace_bytes < ancha_hip_istft_workspace(frames) || !aligned16(workspace))
+    return ANCHA_HIP_INVALID;
+  float* frames_buf = static_cast<float*>(workspace);
+  const long n = static_cast<long>(length);
+  hipError_t e = ancha::launch_zero(out, 2 * n, stream);
+  if (e == hipSuccess)
+    e = ancha::launch_istft_frames(spectrum, masks, static_cast<int>(frames), zero_dc ? 1 : 0,
+                                   frames_buf, stream);
+  // One chunk covering the whole output: unit fade weights (first and last).
+  if (e == hipSuccess)
+    e = ancha::launch_ola_accumulate(frames_buf, static_cast<int>(frames), static_cast<int>(hop),
+                                     n, 0, n, true, true, false, out, nullptr, stream);
+  return e == hipSuccess ? 0 : -static_cast<int>(e);
+}
+
+}  // extern "C"

@@ -108,6 +108,106 @@ def axis_rope_packed(freqs: np.ndarray, tokens: int) -> np.ndarray:
     return np.stack([cos2 * scale, sin2 * scale, cos2, sin2]).astype(np.float32)
 
 
+def roformer_tensor_shapes(config: dict) -> dict:
+    """Checkpoint tensor names and shapes of a Mel/BS-RoFormer (network.rs:96-177,
+    roformer.rs:205-252 and :381-409), in a fixed order."""
+    dim, heads, hd = config["dim"], config["heads"], config["head_dim"]
+    inner, hidden = heads * hd, dim * config["ff_mult"]
+    mh = dim * config["mask_expansion"]
+    mel = config["family"] == "mel-band-roformer"
+    shapes = {}
+    for b, bins in enumerate(config["bands"]):
+        w = 4 * len(bins)
+        p = f"band_split.to_features.{b}"
+        shapes[f"{p}.0.gamma"] = (w,)
+        shapes[f"{p}.1.weight"] = (dim, w)
+        shapes[f"{p}.1.bias"] = (dim,)
+    for i in range(config["depth"]):
+        for axis in range(2):
+            p = f"layers.{i}.{axis}"
+            a, f = f"{p}.layers.0.0", f"{p}.layers.0.1.net"
+            shapes[f"{a}.norm.gamma"] = (dim,)
+            shapes[f"{a}.to_qkv.weight"] = (3 * inner, dim)
+            shapes[f"{a}.to_gates.weight"] = (heads, dim)
+            shapes[f"{a}.to_gates.bias"] = (heads,)
+            shapes[f"{a}.to_out.0.weight"] = (dim, inner)
+            shapes[f"{a}.rotary_embed.freqs"] = (hd // 2,)
+            shapes[f"{f}.0.gamma"] = (dim,)
+            shapes[f"{f}.1.weight"] = (hidden, dim)
+            shapes[f"{f}.1.bias"] = (hidden,)
+            shapes[f"{f}.4.weight"] = (dim, hidden)
+            shapes[f"{f}.4.bias"] = (dim,)
+            if mel:
+                shapes[f"{p}.norm.gamma"] = (dim,)
+    if not mel:
+        shapes["final_norm.gamma"] = (dim,)
+    layers = config["mask_depth"] if mel else config["mask_depth"] - 1
+    for s in range(len(config["stems"])):
+        for b, bins in enumerate(config["bands"]):
+            p = f"mask_estimators.{s}.to_freqs.{b}.0"
+            fan_in = dim
+            for layer in range(layers):
+                shapes[f"{p}.{2 * layer}.weight"] = (mh, fan_in)
+                shapes[f"{p}.{2 * layer}.bias"] = (mh,)
+                fan_in = mh
+            shapes[f"{p}.{2 * layers}.weight"] = (8 * len(bins), mh)
+            shapes[f"{p}.{2 * layers}.bias"] = (8 * len(bins),)
+    return shapes
+
+
+def roformer_tensors(config: dict, seed: int = SEED_WEIGHTS, scale: float = 0.02,
+                     device=None) -> dict:
+    """Random-init checkpoint: gammas 1, rotary frequencies theta = 10000, every other tensor
+    N(0, scale^2) from one seeded stream, consumed in roformer_tensor_shapes order. With a
+    torch `device` the stream is generated there (same values) and copied back."""
+    shapes = roformer_tensor_shapes(config)
+    random = [(n, s) for n, s in shapes.items() if not n.endswith(("gamma", "freqs"))]
+    total = sum(int(np.prod(s)) for _, s in random)
+    if device is not None:
+        flat = normal_torch((total,), seed, scale, device=device).cpu().numpy()
+    else:
+        flat = normal((total,), seed, scale)
+    out, first = {}, 0
+    for name, shape in shapes.items():
+        if name.endswith("gamma"):
+            out[name] = np.ones(shape, np.float32)
+        elif name.endswith("freqs"):
+            out[name] = rope_freqs(2 * shape[0])
+        else:
+            size = int(np.prod(shape))
+            out[name] = flat[first:first + size].reshape(shape)
+            first += size
+    return out
+
+
+def audio(samples: int, seed: int = SEED_AUDIO, sample_rate: int = 44100) -> np.ndarray:
+    """Stereo test audio [2, samples]: pink noise (Paul Kellet's filter on a seeded N(0, 1)
+    stream, scaled to ~0.1 RMS) plus three sines at seeded frequencies and amplitudes."""
+    from scipy.signal import lfilter
+
+    white = normal((2, samples), seed, 1.0).astype(np.float64)
+    out = np.empty((2, samples), np.float64)
+    poles = (0.99886, 0.99332, 0.96900, 0.86650, 0.55000, -0.7616)
+    gains = (0.0555179, 0.0750759, 0.1538520, 0.3104856, 0.5329522, -0.0168980)
+    for c in range(2):
+        w = white[c]
+        y = w * 0.5362
+        for a, g in zip(poles, gains):  # b_k[n] = a b_k[n-1] + g w[n]
+            y = y + lfilter([g], [1.0, -a], w)
+        y[1:] += 0.115926 * w[:-1]  # b_6: the previous sample's 0.115926 w
+        out[c] = y * (0.1 / max(np.std(y), 1e-12))
+    params = normal((3, 3), seed + 1, 1.0).astype(np.float64)
+    t = np.arange(samples) / sample_rate
+    for k in range(3):
+        freq = 110.0 * 2.0 ** (abs(params[k, 0]) * 2.0)
+        amp = 0.05 + 0.05 * abs(params[k, 1])
+        phase = params[k, 2]
+        tone = amp * np.sin(2 * np.pi * freq * t + phase)
+        out[0] += tone
+        out[1] += tone * (0.8 if k % 2 else 1.0)
+    return out.astype(np.float32)
+
+
 def attention_inputs(shape, scale: float = 1.0 / 8.0):
     """q, k, v float32 [G, T, H, 64] ~ N(0, scale^2) from seeds 1, 2, 3 (token-major order)."""
     return tuple(normal(shape, seed, scale) for seed in (SEED_Q, SEED_K, SEED_V))

@@ -162,6 +162,76 @@ int ancha_hip_axis_pair_forward(const ancha_hip_block *time, const ancha_hip_blo
                                 const float *time_rope, const float *band_rope, void *workspace,
                                 size_t workspace_bytes, float *out, hipStream_t stream);
 
+/* ---- Mel/BS-RoFormer network and separation runtime around the attention path ---- */
+
+/* Model configuration: the fields of ModelConfig (crates/ancha-models/src/config.rs:14-32).
+ * Band b covers FFT bins band_bins[band_offsets[b] .. band_offsets[b+1]) (strictly increasing
+ * within a band; every bin covered). n_fft must be 2048 and head_dim 64. */
+typedef struct {
+  int mel;               /* 1: Mel-Band-RoFormer (per-block output norms), 0: BS-RoFormer */
+  size_t dim, depth, heads, head_dim, ff_mult, mask_depth, mask_expansion;
+  size_t n_fft, hop, chunk_samples, overlap;
+  int zero_dc;
+  size_t stems, bands;
+  const size_t *band_offsets; /* [bands + 1] */
+  const size_t *band_bins;    /* [band_offsets[bands]] */
+} ancha_hip_roformer_config;
+
+/* Serves the checkpoint tensor `name` (the reference's safetensors names, e.g.
+ * "band_split.to_features.3.1.weight") as `numel` host fp32 values, or NULL when absent. The
+ * pointer must stay valid until ancha_hip_roformer_create returns. */
+typedef const float *(*ancha_hip_tensor_fn)(void *ctx, const char *name, size_t numel);
+
+typedef struct ancha_hip_roformer ancha_hip_roformer;
+
+/* Loads the network on the current device: band-split projections (sqrt(width)*gamma folded),
+ * depth x (time, frequency) blocks, BS final norm, per-stem mask heads (fp16 weights, output
+ * projections padded to multiples of 128 columns). INVALID for a config the schema rejects or
+ * a missing tensor, UNSUPPORTED for shapes outside the kernels.
+ * Replaces `Roformer::load` / `Roformer::build` (crates/ancha-models/src/network.rs:79-278). */
+int ancha_hip_roformer_create(const ancha_hip_roformer_config *config, ancha_hip_tensor_fn get,
+                              void *ctx, ancha_hip_roformer **model);
+
+/* Device bytes of the workspace ancha_hip_roformer_forward needs for `frames` frames. */
+size_t ancha_hip_roformer_workspace(const ancha_hip_roformer *model, size_t frames);
+
+/* masks [stems][2 * 1025][re, im][frames] = model(spectrum [frames][1025][channel][re, im]):
+ * band split -> axis loop (the frequency pass reads the time layout in place) -> mask heads
+ * (tanh hidden layers, GLU, overlapping-band average). The first call with a new frame count
+ * builds that count's rotary tables (device allocation); other calls allocate nothing.
+ * Replaces `Roformer::forward` (network.rs:303-400). */
+int ancha_hip_roformer_forward(ancha_hip_roformer *model, const float *spectrum, size_t frames,
+                               void *workspace, size_t workspace_bytes, float *masks,
+                               hipStream_t stream);
+
+/* Device bytes of the workspace ancha_hip_separate needs for a clip of `samples` samples. */
+size_t ancha_hip_separate_workspace(const ancha_hip_roformer *model, size_t samples);
+
+/* stems [stems][2][samples] (and, for one-stem models, residual [2][samples] = audio - stem, or
+ * NULL) from stereo audio [2][samples], all device memory: reflect-bordered chunks every
+ * chunk_samples / overlap samples, STFT, forward, complex masks, iSTFT, fade-weighted
+ * overlap-add, border crop. Allocates nothing.
+ * Replaces the chunk loop of src/runtime.rs:103-238 (+ residual_audio, :403-420). */
+int ancha_hip_separate(ancha_hip_roformer *model, const float *audio, size_t samples,
+                       void *workspace, size_t workspace_bytes, float *stems, float *residual,
+                       hipStream_t stream);
+
+void ancha_hip_roformer_destroy(ancha_hip_roformer *model);
+
+/* Stft::forward (crates/ancha-audio/src/dsp.rs:46-84) of both channels of signal
+ * [2][samples]: spectrum [samples / hop + 1][1025][channel][re, im] (n_fft 2048, periodic
+ * Hann, reflect padding, unnormalised). */
+int ancha_hip_stft(const float *signal, size_t samples, size_t hop, float *spectrum,
+                   hipStream_t stream);
+
+size_t ancha_hip_istft_workspace(size_t frames);
+
+/* Stft::inverse (dsp.rs:86-134) of spectrum * masks for both channels: spectrum as above,
+ * masks [2 * 1025][re, im][frames] (complex, per row 2*bin + channel), out [2][length]. */
+int ancha_hip_istft(const float *spectrum, const float *masks, size_t frames, size_t hop,
+                    size_t length, int zero_dc, void *workspace, size_t workspace_bytes,
+                    float *out, hipStream_t stream);
+
 /* Sticky device-failure check: 0, or the first HIP error (< 0) any call has met.
  * Replaces `device::check()` (src/device.rs:30-41) for this path. */
 int ancha_hip_check(void);

@@ -122,6 +122,25 @@ typedef struct {
 int anc_transformer_forward(const anc_block_weights *w, const float *x, size_t groups,
                             size_t tokens, int kernels, size_t threads, float *out);
 
+/* ---- mel_oracle.c: Mel/BS-RoFormer front end, mask estimator and STFT ---- */
+
+/* crates/ancha-audio/src/dsp.rs:139-147 */
+size_t anc_reflect_index(long index, size_t length);
+/* dsp.rs:46-84 Stft::forward: out [n / hop + 1][n_fft / 2 + 1][re, im]. */
+int anc_stft(const float *signal, size_t n, size_t n_fft, size_t hop, float *out);
+/* dsp.rs:86-134 Stft::inverse: spectrum [frames][n_fft / 2 + 1][re, im] -> out [length]. */
+int anc_istft(const float *spectrum, size_t frames, size_t n_fft, size_t hop, size_t length,
+              int zero_dc, float *out);
+/* crates/ancha-models/src/network.rs:316-323 (+ :96-121 folding): x [bands][t][dim]. */
+int anc_band_split(const float *spectrum, size_t t, size_t cols, size_t bands,
+                   const size_t *offsets, const size_t *bins, size_t dim, const float *gamma,
+                   const float *weight, const float *bias, size_t threads, float *x);
+/* network.rs:138-177 + :365-398: one stem's masks [2 * fft_bins][2][t]. */
+int anc_mask_head(const float *x, size_t t, size_t bands, const size_t *offsets,
+                  const size_t *bins, size_t fft_bins, size_t dim, size_t hidden, size_t layers,
+                  const float *const *hw, const float *const *hb, const float *ow,
+                  const float *ob, size_t threads, float *masks);
+
 #ifdef __cplusplus
 }
 #endif
