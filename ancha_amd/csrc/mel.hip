@@ -17,48 +17,90 @@
 namespace ancha {
 namespace {
 
-constexpr int kSplitFrames = 16;     // frames per workgroup at most
+constexpr int kSplitFrames = 16;   // frames per workgroup
 constexpr int kSplitThreads = 256;
-constexpr int kSplitLds = 48 * 1024;  // LDS for the gathered features
+constexpr int kSplitCols = 512;    // feature columns staged per pass (32 KB of LDS)
+constexpr int kSplitDims = 4;      // output channels per thread (one float4 of W')
+constexpr int kSplitJobs = 2 * 512 / kSplitDims;  // (channel group, frame half) pairs, dim <= 512
 
+// Thread job (dg, half): channels 4*dg .. 4*dg+3 for frames 8*half .. 8*half+7 of the tile.
+// The band's features pass through LDS transposed, zt[column][frame], kSplitCols columns at a
+// time, so a thread reads its 8 frames of a column as two 16-byte words and its 4 weights as
+// one: 32 FMAs per 3 loads. Squared norms accumulate over the passes; 1/norm is applied last.
 __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitParams p) {
-  extern __shared__ float z[];  // [tile][max_width] then inv[tile]
-  const int tile = p.tile;     // frames per workgroup: kSplitLds / (4 * max_width), <= 16
-  const int b = blockIdx.x, t0 = blockIdx.y * tile;
+  __shared__ __attribute__((aligned(16))) float zt[kSplitCols * kSplitFrames];
+  __shared__ float sq[kSplitFrames];
+  const int b = blockIdx.x, t0 = blockIdx.y * kSplitFrames;
   const int q0 = p.offsets[b], nb = p.offsets[b + 1] - q0, width = 4 * nb;
-  const int frames = min(tile, p.frames - t0);
-  float* inv = z + tile * p.max_width;
-  // Gather: one float4 (the bin's 4 columns) per (frame, bin).
-  for (int e = threadIdx.x; e < frames * nb; e += kSplitThreads) {
-    const int tt = e / nb, q = e % nb;
-    const float4 v = *reinterpret_cast<const float4*>(
-        p.spectrum + (long)(t0 + tt) * p.cols + 4 * p.bins[q0 + q]);
-    *reinterpret_cast<float4*>(z + tt * p.max_width + 4 * q) = v;
-  }
-  __syncthreads();
-  // Row norms: wave w takes frames w, w + 4, ...
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  for (int tt = wave; tt < frames; tt += kSplitThreads / 64) {
-    float s = 0.0f;
-    for (int c = lane; c < width; c += 64) s += z[tt * p.max_width + c] * z[tt * p.max_width + c];
-    for (int o = 32; o > 0; o >>= 1) s += __shfl_xor(s, o);
-    if (lane == 0) inv[tt] = 1.0f / fmaxf(sqrtf(s), 1e-12f);
-  }
-  __syncthreads();
+  const int frames = min(kSplitFrames, p.frames - t0);
   const float* w = p.weight + (long)p.wofs[b] * p.dim;
-  for (int d = threadIdx.x; d < p.dim; d += kSplitThreads) {
-    float acc[kSplitFrames];
+  const int groups = p.dim / kSplitDims;
+  if (threadIdx.x < kSplitFrames) sq[threadIdx.x] = 0.0f;
+  float acc[2][8][kSplitDims];  // the thread's (up to) two jobs
 #pragma unroll
-    for (int tt = 0; tt < kSplitFrames; tt++) acc[tt] = 0.0f;
-    for (int c = 0; c < width; c++) {
-      const float wc = w[(long)c * p.dim + d];
+  for (int r = 0; r < 2; r++)
 #pragma unroll
-      for (int tt = 0; tt < kSplitFrames; tt++)
-        if (tt < frames) acc[tt] += wc * z[tt * p.max_width + c];
+    for (int i = 0; i < 8; i++)
+#pragma unroll
+      for (int j = 0; j < kSplitDims; j++) acc[r][i][j] = 0.0f;
+  for (int c0 = 0; c0 < width; c0 += kSplitCols) {
+    const int cols = min(kSplitCols, width - c0), bins = cols / 4;
+    __syncthreads();  // the previous pass is done with zt
+    for (int e = threadIdx.x; e < kSplitFrames * bins; e += kSplitThreads) {
+      const int tt = e % kSplitFrames, q = e / kSplitFrames;
+      float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (tt < frames)
+        v = *reinterpret_cast<const float4*>(p.spectrum + (long)(t0 + tt) * p.cols +
+                                             4 * p.bins[q0 + c0 / 4 + q]);
+      zt[(4 * q + 0) * kSplitFrames + tt] = v.x;
+      zt[(4 * q + 1) * kSplitFrames + tt] = v.y;
+      zt[(4 * q + 2) * kSplitFrames + tt] = v.z;
+      zt[(4 * q + 3) * kSplitFrames + tt] = v.w;
     }
-    const float bias = p.bias[(long)b * p.dim + d];
-    for (int tt = 0; tt < frames; tt++)
-      p.x[((long)b * p.frames + t0 + tt) * p.dim + d] = acc[tt] * inv[tt] + bias;
+    __syncthreads();
+    {  // squared norms: 16 lanes per frame
+      const int tt = threadIdx.x >> 4, l = threadIdx.x & 15;
+      float s = 0.0f;
+      for (int c = l; c < cols; c += 16) s += zt[c * kSplitFrames + tt] * zt[c * kSplitFrames + tt];
+      for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o);
+      if (l == 0) sq[tt] += s;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+      const int job = threadIdx.x + r * kSplitThreads;
+      if (job >= 2 * groups) break;
+      const int dg = job % groups, half = job / groups, d0 = kSplitDims * dg;
+      const float* zc = zt + half * 8;
+      const float* wc = w + (long)c0 * p.dim + d0;
+#pragma unroll 4
+      for (int c = 0; c < cols; c++) {
+        const float4 wv = *reinterpret_cast<const float4*>(wc + (long)c * p.dim);
+        const float4 za = *reinterpret_cast<const float4*>(zc + c * kSplitFrames);
+        const float4 zb = *reinterpret_cast<const float4*>(zc + c * kSplitFrames + 4);
+        const float zz[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
+        const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int i = 0; i < 8; i++)
+#pragma unroll
+          for (int j = 0; j < kSplitDims; j++) acc[r][i][j] += ww[j] * zz[i];
+      }
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 2; r++) {
+    const int job = threadIdx.x + r * kSplitThreads;
+    if (job >= 2 * groups) break;
+    const int dg = job % groups, half = job / groups, d0 = kSplitDims * dg;
+    const float4 bias = *reinterpret_cast<const float4*>(p.bias + (long)b * p.dim + d0);
+    for (int i = 0; i < 8; i++) {
+      const int tt = half * 8 + i;
+      if (tt >= frames) break;
+      const float s = 1.0f / fmaxf(sqrtf(sq[tt]), 1e-12f);
+      *reinterpret_cast<float4*>(p.x + ((long)b * p.frames + t0 + tt) * p.dim + d0) =
+          make_float4(acc[r][i][0] * s + bias.x, acc[r][i][1] * s + bias.y,
+                      acc[r][i][2] * s + bias.z, acc[r][i][3] * s + bias.w);
+    }
   }
 }
 
@@ -83,11 +125,10 @@ __global__ void glu_gather_kernel(GluParams p) {
 
 hipError_t launch_band_split(const BandSplitParams& params, hipStream_t stream) {
   BandSplitParams p = params;
-  if (p.max_width <= 0 || 4 * p.max_width > kSplitLds) return hipErrorInvalidValue;
-  p.tile = min(kSplitFrames, kSplitLds / (4 * p.max_width));
-  const dim3 grid(p.bands, (p.frames + p.tile - 1) / p.tile);
-  const size_t lds = sizeof(float) * ((size_t)p.tile * p.max_width + p.tile);
-  hipLaunchKernelGGL(band_split_kernel, grid, dim3(kSplitThreads), lds, stream, p);
+  if (p.dim % kSplitDims || 2 * p.dim / kSplitDims > kSplitJobs) return hipErrorInvalidValue;
+  p.tile = kSplitFrames;
+  const dim3 grid(p.bands, (p.frames + kSplitFrames - 1) / kSplitFrames);
+  hipLaunchKernelGGL(band_split_kernel, grid, dim3(kSplitThreads), 0, stream, p);
   return hipGetLastError();
 }
 

@@ -333,8 +333,8 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
   for (int n : coverage)
     if (n == 0) return ANCHA_HIP_INVALID;  // "bands leave uncovered FFT bins"
   const size_t dim = c->dim, mh = c->dim * c->mask_expansion;
-  if (!ancha_hip_linear_supported(dim, mh) || !ancha_hip_linear_supported(mh, mh))
-    return ANCHA_HIP_UNSUPPORTED;
+  if (!ancha_hip_linear_supported(dim, mh) || !ancha_hip_linear_supported(mh, mh) || dim > 512)
+    return ANCHA_HIP_UNSUPPORTED;  // (the band-split kernel covers dim <= 512)
 
   auto* m = new (std::nothrow) ancha_hip_roformer{};
   if (!m) return ANCHA_HIP_INVALID;

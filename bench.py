@@ -11,7 +11,10 @@ Prints ONE JSON line: throughput in TFLOP/s (4*G*H*T^2*d per call), the live roo
 attention kernel (HIP events over the timed region on the launch stream) and the restated
 reference CPU path (the oracle's materialized-tile attention) timed on the host's cores.
 
-`--workload band` measures the band-axis op [1602, 60, 8, 64] instead (HBM-bound roofline).
+`--workload band` measures the band-axis op [1602, 60, 8, 64] instead (HBM-bound roofline),
+`--workload layer` one RoFormer layer pair on [2, 60, 801, 384], and `--workload mel` the
+Mel-RoFormer separation of a 30 s stereo clip (audio-seconds per second; one step = the whole
+clip: 21 chunks of STFT, network, iSTFT and overlap-add).
 """
 from __future__ import annotations
 
@@ -232,12 +235,107 @@ def layer_cpu_baseline(wt, wb, x, gpu_out, budget_s: float = 12.0) -> dict:
                        f"{len(times)} ({t:.2f} s)")}
 
 
+MEL_CLIP_SECONDS = 30
+
+
+def mel_flops(config: dict) -> float:
+    """Algorithmic FLOPs of one chunk's network forward: band split, depth x (time block on
+    groups = bands, frequency block on groups = frames), mask heads (hidden layers and the
+    value|gate projections). The STFT / iSTFT (O(n log n)) are left out."""
+    frames = config["chunk_samples"] // config["hop"] + 1
+    nb, dim = len(config["bands"]), config["dim"]
+    widths = [4 * len(b) for b in config["bands"]]
+    hidden = dim * config["ff_mult"]
+    mh = dim * config["mask_expansion"]
+    layers = config["mask_depth"] if config["family"] == "mel-band-roformer" \
+        else config["mask_depth"] - 1
+    f = 2.0 * frames * sum(widths) * dim
+    f += config["depth"] * (layer_flops(nb, frames, dim, config["heads"], hidden)
+                            + layer_flops(frames, nb, dim, config["heads"], hidden))
+    head = 2.0 * frames * nb * (dim * mh + (layers - 1) * mh * mh) + 2.0 * frames * sum(
+        2 * w for w in widths) * mh
+    return f + len(config["stems"]) * head
+
+
+def run_mel(args, torch, dev) -> int:
+    """Mel-RoFormer separation (bundled Mel-Karaoke config, random N(0, 0.02) weights) of a
+    30 s stereo clip resident in HBM."""
+    from ancha_amd import separation as S
+    from ancha_amd import workload as W
+    config = S.load_config("mel_karaoke")
+    sr = config["sample_rate"]
+    n = MEL_CLIP_SECONDS * sr
+    log("generating weights (GPU stream) and the clip")
+    tensors = W.roformer_tensors(config, device=dev)
+    model = S.Roformer(config, tensors, dev)
+    audio_np = W.audio(n)
+    audio = torch.from_numpy(audio_np).to(dev)
+    step = lambda: model.separate(audio)
+    out = step()
+    for _ in range(args.warmup):
+        out = step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(args.steps):
+        out = step()
+    end.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    gpu_ms = start.elapsed_time(end) / args.steps
+    step_ = config["chunk_samples"] // config["overlap"]
+    border = config["chunk_samples"] - step_
+    border = border if n > 2 * border else 0
+    chunks = len(range(0, n + 2 * border, step_))
+    flops = chunks * mel_flops(config)
+    achieved = flops / (gpu_ms * 1e-3) / 1e12
+    log(f"mel separation: {gpu_ms:.1f} ms per {MEL_CLIP_SECONDS} s clip ({chunks} chunks), "
+        f"{MEL_CLIP_SECONDS / (gpu_ms * 1e-3):.1f} audio-s/s, {achieved:.1f} TFLOP/s")
+    result = {
+        "metric": "audio-seconds/sec for Mel-RoFormer fwd",
+        "value": round(MEL_CLIP_SECONDS * args.steps / wall, 3),
+        "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / args.steps, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: seeded pink noise + 3 sines, 30 s stereo 44.1 kHz; weights "
+                "N(0,0.02), gamma 1, rotary theta 10000 (seeded)",
+        "config": {"workload": "Mel-RoFormer separation (Mel-Karaoke: 60 bands, dim 384, depth "
+                               "6, 8x64 heads, chunk 352800 / overlap 4) of a 30 s clip",
+                   "chunks": chunks, "frames_per_chunk": config["chunk_samples"] //
+                   config["hop"] + 1, "gflop_per_clip": round(flops / 1e9, 1),
+                   "mfma_operands": "fp16", "accumulate": "fp32", "dsp": "fp32",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
+                     "traffic": None, "scope": "whole separation (all kernels)"},
+    }
+    if not args.no_cpu_baseline:
+        import oracle.mel as OM
+        threads = cpu_threads()
+        log(f"timing the restated reference CPU path on the first chunk ({threads} threads)")
+        weights = OM.weights_from_tensors(config, tensors)
+        t0 = time.perf_counter()
+        OM.separate(audio_np, config, weights, threads=threads, chunks=1)
+        t = time.perf_counter() - t0
+        result["cpu_baseline"] = {
+            "value": round(MEL_CLIP_SECONDS / chunks / t, 5), "unit": "audio-s/s",
+            "cores": threads, "kind": "port",
+            "sample": (f"first of the clip's {chunks} chunks through the full model (STFT, "
+                       f"band split, 6 layer pairs, mask head, iSTFT, overlap-add), "
+                       f"credited {MEL_CLIP_SECONDS}/{chunks} s of audio ({t:.1f} s)")}
+    del out
+    print(json.dumps(result), flush=True)
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["time", "band", "layer"], default="time")
+    ap.add_argument("--workload", choices=["time", "band", "layer", "mel"], default="time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain device copy of the workload's I/O size instead; its "
@@ -261,6 +359,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.workload == "layer":
         return run_layer(args, torch, dev)
+    if args.workload == "mel":
+        return run_mel(args, torch, dev)
     shape = W.TIME_SHAPE if args.workload == "time" else W.BAND_SHAPE
     G, T, H, D = shape
     log(f"generating q, k, v {shape} on the GPU")

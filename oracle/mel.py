@@ -226,7 +226,8 @@ def separate(audio, config, weights, threads=1, chunks=None):
                 mask = (m[:, 0, :] + 1j * m[:, 1, :]).T.astype(np.complex64)
                 planes.append(istft(spectra[c] * mask, cs, n_fft, hop, config["zero_dc"]))
         acc.add(start, planes)
-    out = acc.finish().reshape(stems, 2, length)
+    # A timing sample (`chunks`) leaves later samples uncovered: divide where covered.
+    out = acc.finish(strict=chunks is None).reshape(stems, 2, length)
     return out[..., border:border + n]
 
 
@@ -247,7 +248,10 @@ class OverlapAdd:
         for c, plane in enumerate(planes):
             self.sums[c, start:end] += w * np.asarray(plane, np.float32)[: end - start]
 
-    def finish(self) -> np.ndarray:
-        if not np.all(self.weights > 0):
+    def finish(self, strict: bool = True) -> np.ndarray:
+        covered = self.weights > 0
+        if strict and not np.all(covered):
             raise ValueError("uncovered overlap-add sample")
-        return self.sums / self.weights
+        out = np.zeros_like(self.sums)
+        out[:, covered] = self.sums[:, covered] / self.weights[covered]
+        return out
