@@ -57,6 +57,11 @@ __device__ __forceinline__ u32x4 p_fragment(f32x4 a, f32x4 b) {
                pack_h2(b[2], b[3])};
 }
 
+// Dword j (keys a, b of channel j) of a V^T chunk from the fp16 channels 4c .. 4c+3 of two keys.
+__device__ __forceinline__ unsigned v_pair(u32x2 a, u32x2 b, int j) {
+  return __builtin_amdgcn_perm(b[j >> 1], a[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
+}
+
 // First row of group g (token 0) in q/k/v/gate/out; token t adds t * p.tstep rows.
 __device__ __forceinline__ long group_row(const AttnParams& p, int g) {
   return (long)(g / p.gsplit) * p.gouter + (long)(g % p.gsplit) * p.gstep;
@@ -66,7 +71,7 @@ __device__ __forceinline__ long group_row(const AttnParams& p, int g) {
 struct OutRows {
   rsrc_t out, gate;
   unsigned ld4, ldg4;
-  bool half;
+  bool half, gate_half;
 };
 
 __device__ __forceinline__ OutRows out_rows(const AttnParams& p, int g, int h) {
@@ -78,9 +83,13 @@ __device__ __forceinline__ OutRows out_rows(const AttnParams& p, int g, int h) {
   o.ld4 = (unsigned)(p.tstep * p.heads * 64 * esize);
   o.out = make_rsrc(reinterpret_cast<unsigned char*>(p.out) + (row * p.heads + h) * 64 * esize,
                     (unsigned)(T - 1) * o.ld4 + 64 * esize);
-  o.ldg4 = (unsigned)(p.tstep * p.ldg * 4);
-  o.gate = make_rsrc(p.gate ? p.gate + row * p.ldg + h : p.out,
-                     p.gate ? (unsigned)(T - 1) * o.ldg4 + 4 : 0);
+  o.gate_half = p.in_half != 0;
+  const unsigned gsize = o.gate_half ? 2 : 4;
+  o.ldg4 = (unsigned)(p.tstep * p.ldg * gsize);
+  o.gate = make_rsrc(p.gate ? reinterpret_cast<const unsigned char*>(p.gate) +
+                                  (row * p.ldg + h) * gsize
+                            : reinterpret_cast<const unsigned char*>(p.out),
+                     p.gate ? (unsigned)(T - 1) * o.ldg4 + gsize : 0);
   return o;
 }
 
@@ -89,7 +98,13 @@ template <bool GATED, bool ALIGNED>
 __device__ __forceinline__ void store_output(const OutRows& o, const f32x4 (&acc)[4], float l,
                                              int t, int grp) {
   float scale = 1.0f / l;
-  if constexpr (GATED) scale = scale / (1.0f + expf(-bload1(o.gate, (unsigned)t * o.ldg4)));
+  if constexpr (GATED) {
+    const float gl =
+        o.gate_half ? (float)__builtin_bit_cast(
+                          _Float16, __builtin_amdgcn_raw_buffer_load_b16(o.gate, (unsigned)t * o.ldg4, 0, 0))
+                    : bload1(o.gate, (unsigned)t * o.ldg4);
+    scale = scale / (1.0f + expf(-gl));
+  }
   if (o.half) {
     const unsigned base = (unsigned)t * o.ld4 + grp * 8;
 #pragma unroll
@@ -138,7 +153,7 @@ __device__ __forceinline__ void scale_in_place(f32x4& acc, float s) {
 constexpr int kTimeWaves = 8;
 constexpr int kTimeQueries = kTimeWaves * 64;
 
-template <bool GATED, bool ROPE, bool ALIGNED>
+template <bool GATED, bool ROPE, bool ALIGNED, bool XH>
 __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnParams p, int qblocks,
                                                                          int total) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_k[2][64 * 128];
@@ -152,10 +167,14 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   const int h = gh % p.heads, g = gh / p.heads;
   const int T = p.tokens;
   const long row0 = group_row(p, g), ts = p.tstep;
-  const unsigned ldq4 = (unsigned)(ts * p.ldq * 4), ldk4 = (unsigned)(ts * p.ldk * 4),
-                 ldv4 = (unsigned)(ts * p.ldv * 4);
-  const float* kbase = p.k + row0 * p.ldk + h * 64;
-  const float* vbase = p.v + row0 * p.ldv + h * 64;
+  // XH: fp16 q / k / v rows (64 * 2 bytes per head), else fp32.
+  constexpr unsigned kEsz = XH ? 2 : 4, kRowBytes = 64 * kEsz;
+  const unsigned ldq4 = (unsigned)(ts * p.ldq * kEsz), ldk4 = (unsigned)(ts * p.ldk * kEsz),
+                 ldv4 = (unsigned)(ts * p.ldv * kEsz);
+  const unsigned char* kbase =
+      reinterpret_cast<const unsigned char*>(p.k) + (row0 * p.ldk + h * 64) * kEsz;
+  const unsigned char* vbase =
+      reinterpret_cast<const unsigned char*>(p.v) + (row0 * p.ldv + h * 64) * kEsz;
   const int q0 = qblk * kTimeQueries + wave * 64;
   const bool active = q0 < T;
 
@@ -172,10 +191,23 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   const unsigned toff = (unsigned)lrow * 256 + lchunk * 16;
   float4 kreg[2], vreg[2];
   float4 kcos[2], ksin[2];
+  // fp16 staging: thread owns the 16-byte chunk tid & 7 of K row tid >> 3, and the same V
+  // block as above as two 8-byte rows.
+  u32x4 kh;
+  u32x2 vh[2];
   auto load_tile = [&](int key0) {
     const unsigned rows = (unsigned)(T - key0);
-    const rsrc_t kr = make_rsrc(kbase + key0 * ts * p.ldk, (rows - 1) * ldk4 + 256);
-    const rsrc_t vr = make_rsrc(vbase + key0 * ts * p.ldv, (rows - 1) * ldv4 + 256);
+    const rsrc_t kr = make_rsrc(kbase + (long)key0 * ldk4, (rows - 1) * ldk4 + kRowBytes);
+    const rsrc_t vr = make_rsrc(vbase + (long)key0 * ldv4, (rows - 1) * ldv4 + kRowBytes);
+    if constexpr (XH) {
+      kh = __builtin_amdgcn_raw_buffer_load_b128(kr, (unsigned)(tid >> 3) * ldk4 + (tid & 7) * 16,
+                                                 0, 0);
+#pragma unroll
+      for (int r = 0; r < 2; r++)
+        vh[r] = __builtin_amdgcn_raw_buffer_load_b64(vr, (unsigned)(2 * lrow + r) * ldv4 + lchunk * 8,
+                                                     0, 0);
+      return;
+    }
 #pragma unroll
     for (int it = 0; it < 2; it++) kreg[it] = bload4<ALIGNED>(kr, koff + it * 32 * ldk4);
 #pragma unroll
@@ -193,6 +225,14 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
     }
   };
   auto store_tile = [&](int buf) {
+    if constexpr (XH) {
+      *reinterpret_cast<u32x4*>(lds_k[buf] + k_offset(tid >> 3, tid & 7)) = kh;
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        *reinterpret_cast<unsigned*>(lds_v[buf] + vtc_offset(lchunk * 4 + j, 2 * lrow)) =
+            v_pair(vh[0], vh[1], j);
+      return;
+    }
 #pragma unroll
     for (int it = 0; it < 2; it++) {
       const int r = lrow + 32 * it;
@@ -228,12 +268,23 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
     // Stage this wave's 64 query rows: coalesced row loads (16 lanes per 256-byte row), RoPE
     // with the query table rows (carrying 1/sqrt(64)), log2(e), fp16, into the K-tile layout.
     const unsigned rows = (unsigned)(T - q0);
-    const rsrc_t qr = make_rsrc(p.q + (row0 + q0 * ts) * p.ldq + h * 64, (rows - 1) * ldq4 + 256);
+    const rsrc_t qr = make_rsrc(reinterpret_cast<const unsigned char*>(p.q) +
+                                    ((row0 + q0 * ts) * p.ldq + h * 64) * kEsz,
+                                (rows - 1) * ldq4 + kRowBytes);
     const rsrc_t cr = make_rsrc(ROPE ? p.rope + (long)q0 * 64 : p.q, ROPE ? rows * 256 : 0);
     const rsrc_t sr = make_rsrc(ROPE ? p.rope + (long)(T + q0) * 64 : p.q, ROPE ? rows * 256 : 0);
     const int chunk = lane & 15;
+    if constexpr (XH) {
+      // Already scaled fp16 rows: 8 rows of eight 16-byte chunks per pass.
 #pragma unroll
-    for (int it = 0; it < 16; it++) {
+      for (int it = 0; it < 8; it++) {
+        const int r = it * 8 + (lane >> 3);
+        *reinterpret_cast<u32x4*>(Q + k_offset(r, lane & 7)) =
+            __builtin_amdgcn_raw_buffer_load_b128(qr, (unsigned)r * ldq4 + (lane & 7) * 16, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < (XH ? 0 : 16); it++) {
       const int r = it * 4 + (lane >> 4);
       float4 x = bload4<ALIGNED>(qr, (unsigned)r * ldq4 + chunk * 16);
       if constexpr (ROPE) {
@@ -432,7 +483,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
 // an exact softmax. Small workgroups with few registers keep many problems' loads in flight
 // per CU, which is what this HBM-bound shape needs.
 // ------------------------------------------------------------------------------------------
-template <bool GATED, bool ROPE, bool ALIGNED>
+template <bool GATED, bool ROPE, bool ALIGNED, bool XH>
 __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int problems) {
   __shared__ __attribute__((aligned(16))) unsigned char lds_q[64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_k[64 * 128];
@@ -444,50 +495,87 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   const int h = prob % p.heads, g = prob / p.heads;
   const int T = p.tokens;
   const long row0 = group_row(p, g), ts = p.tstep;
-  const unsigned ldq4 = (unsigned)(ts * p.ldq * 4), ldk4 = (unsigned)(ts * p.ldk * 4),
-                 ldv4 = (unsigned)(ts * p.ldv * 4);
-  const rsrc_t qr = make_rsrc(p.q + row0 * p.ldq + h * 64, (unsigned)(T - 1) * ldq4 + 256);
-  const rsrc_t kr = make_rsrc(p.k + row0 * p.ldk + h * 64, (unsigned)(T - 1) * ldk4 + 256);
-  const rsrc_t vr = make_rsrc(p.v + row0 * p.ldv + h * 64, (unsigned)(T - 1) * ldv4 + 256);
+  constexpr unsigned kEsz = XH ? 2 : 4, kRowBytes = 64 * kEsz;
+  const unsigned ldq4 = (unsigned)(ts * p.ldq * kEsz), ldk4 = (unsigned)(ts * p.ldk * kEsz),
+                 ldv4 = (unsigned)(ts * p.ldv * kEsz);
+  auto rows_of = [&](const float* base, long ld, unsigned ld4) {
+    return make_rsrc(reinterpret_cast<const unsigned char*>(base) + (row0 * ld + h * 64) * kEsz,
+                     (unsigned)(T - 1) * ld4 + kRowBytes);
+  };
+  const rsrc_t qr = rows_of(p.q, p.ldq, ldq4);
+  const rsrc_t kr = rows_of(p.k, p.ldk, ldk4);
+  const rsrc_t vr = rows_of(p.v, p.ldv, ldv4);
 
   // Staging: q / k rows srow + 16*it at channels 4*sc; v key pairs (2*(srow + 16*it), +1),
   // it < 2. Rows at or past T read as 0.
   const int srow = tid >> 4, sc = tid & 15;
-  float4 xq[4], xk[4], xv[4];
+  if constexpr (XH) {
+    // fp16 rows (q already scaled): q / k rows (tid >> 3) + 32*it as 16-byte chunks tid & 7,
+    // v key pairs at 8-byte channel groups sc.
+    u32x4 hq[2], hk[2];
+    u32x2 hv[4];
 #pragma unroll
-  for (int it = 0; it < 4; it++) {
-    const unsigned r = (unsigned)(srow + 16 * it);
-    xq[it] = bload4<ALIGNED>(qr, r * ldq4 + sc * 16);
-    xk[it] = bload4<ALIGNED>(kr, r * ldk4 + sc * 16);
-  }
+    for (int it = 0; it < 2; it++) {
+      const unsigned r = (unsigned)((tid >> 3) + 32 * it);
+      hq[it] = __builtin_amdgcn_raw_buffer_load_b128(qr, r * ldq4 + (tid & 7) * 16, 0, 0);
+      hk[it] = __builtin_amdgcn_raw_buffer_load_b128(kr, r * ldk4 + (tid & 7) * 16, 0, 0);
+    }
 #pragma unroll
-  for (int it = 0; it < 2; it++)
+    for (int it = 0; it < 2; it++)
 #pragma unroll
-    for (int r = 0; r < 2; r++)
-      xv[it * 2 + r] = bload4<ALIGNED>(vr, (unsigned)(2 * (srow + 16 * it) + r) * ldv4 + sc * 16);
-  if constexpr (ROPE) {
-    const rsrc_t tr = make_rsrc(p.rope, (unsigned)T * 1024);
+      for (int r = 0; r < 2; r++)
+        hv[it * 2 + r] = __builtin_amdgcn_raw_buffer_load_b64(
+            vr, (unsigned)(2 * (srow + 16 * it) + r) * ldv4 + sc * 8, 0, 0);
+#pragma unroll
+    for (int it = 0; it < 2; it++) {
+      const int off = k_offset((tid >> 3) + 32 * it, tid & 7);
+      *reinterpret_cast<u32x4*>(lds_q + off) = hq[it];
+      *reinterpret_cast<u32x4*>(lds_k + off) = hk[it];
+    }
+#pragma unroll
+    for (int it = 0; it < 2; it++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+            v_pair(hv[it * 2], hv[it * 2 + 1], j);
+  } else {
+    float4 xq[4], xk[4], xv[4];
 #pragma unroll
     for (int it = 0; it < 4; it++) {
-      const unsigned o = (unsigned)(srow + 16 * it) * 256 + sc * 16, plane = (unsigned)T * 256;
-      xq[it] = rotate4(xq[it], bload4<ALIGNED>(tr, o), bload4<ALIGNED>(tr, o + plane));
-      xk[it] = rotate4(xk[it], bload4<ALIGNED>(tr, o + 2 * plane), bload4<ALIGNED>(tr, o + 3 * plane));
+      const unsigned r = (unsigned)(srow + 16 * it);
+      xq[it] = bload4<ALIGNED>(qr, r * ldq4 + sc * 16);
+      xk[it] = bload4<ALIGNED>(kr, r * ldk4 + sc * 16);
     }
+#pragma unroll
+    for (int it = 0; it < 2; it++)
+#pragma unroll
+      for (int r = 0; r < 2; r++)
+        xv[it * 2 + r] = bload4<ALIGNED>(vr, (unsigned)(2 * (srow + 16 * it) + r) * ldv4 + sc * 16);
+    if constexpr (ROPE) {
+      const rsrc_t tr = make_rsrc(p.rope, (unsigned)T * 1024);
+#pragma unroll
+      for (int it = 0; it < 4; it++) {
+        const unsigned o = (unsigned)(srow + 16 * it) * 256 + sc * 16, plane = (unsigned)T * 256;
+        xq[it] = rotate4(xq[it], bload4<ALIGNED>(tr, o), bload4<ALIGNED>(tr, o + plane));
+        xk[it] = rotate4(xk[it], bload4<ALIGNED>(tr, o + 2 * plane),
+                         bload4<ALIGNED>(tr, o + 3 * plane));
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < 4; it++) {
+      const int r = srow + 16 * it;
+      const float4 q = scale4(xq[it], kLog2e), k = xk[it];
+      const int off = k_offset(r, sc >> 1) + ((sc & 1) << 3);
+      *reinterpret_cast<u32x2*>(lds_q + off) = u32x2{pack_h2(q.x, q.y), pack_h2(q.z, q.w)};
+      *reinterpret_cast<u32x2*>(lds_k + off) = u32x2{pack_h2(k.x, k.y), pack_h2(k.z, k.w)};
+    }
+#pragma unroll
+    for (int it = 0; it < 2; it++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+        *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+            pack_h2(comp(xv[it * 2], j), comp(xv[it * 2 + 1], j));
   }
-#pragma unroll
-  for (int it = 0; it < 4; it++) {
-    const int r = srow + 16 * it;
-    const float4 q = scale4(xq[it], kLog2e), k = xk[it];
-    const int off = k_offset(r, sc >> 1) + ((sc & 1) << 3);
-    *reinterpret_cast<u32x2*>(lds_q + off) = u32x2{pack_h2(q.x, q.y), pack_h2(q.z, q.w)};
-    *reinterpret_cast<u32x2*>(lds_k + off) = u32x2{pack_h2(k.x, k.y), pack_h2(k.z, k.w)};
-  }
-#pragma unroll
-  for (int it = 0; it < 2; it++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-      *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
-          pack_h2(comp(xv[it * 2], j), comp(xv[it * 2 + 1], j));
   __syncthreads();
 
   const int q0 = wave * 16;
@@ -539,17 +627,17 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   store_output<GATED, ALIGNED>(out_rows(p, g, h), o, lsum[0], q0 + col, grp);
 }
 
-template <bool GATED, bool ROPE, bool ALIGNED>
+template <bool GATED, bool ROPE, bool ALIGNED, bool XH = false>
 static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
   const int T = p.tokens;
   if (T <= 64) {
     const int problems = p.groups * p.heads;
-    hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED>), dim3(problems), dim3(256), 0,
-                       stream, p, problems);
+    hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED, XH>), dim3(problems),
+                       dim3(256), 0, stream, p, problems);
   } else {
     const int qblocks = (T + kTimeQueries - 1) / kTimeQueries;
     const int total = p.groups * p.heads * qblocks;
-    hipLaunchKernelGGL((attention_time_kernel<GATED, ROPE, ALIGNED>), dim3(total),
+    hipLaunchKernelGGL((attention_time_kernel<GATED, ROPE, ALIGNED, XH>), dim3(total),
                        dim3(kTimeWaves * 64), 0, stream, p, qblocks, total);
   }
   return hipGetLastError();
@@ -564,6 +652,11 @@ hipError_t launch_attention(const AttnParams& params, bool aligned, hipStream_t 
     p.tstep = 1;
   }
   const bool gated = p.gate != nullptr, rope = p.rope != nullptr;
+  if (p.in_half) {
+    // The block's packed fp16 projection only.
+    if (!gated || rope || !aligned) return hipErrorInvalidValue;
+    return launch_attention_t<true, false, true, true>(p, stream);
+  }
   if (aligned) {
     if (gated) return rope ? launch_attention_t<true, true, true>(p, stream)
                            : launch_attention_t<true, false, true>(p, stream);

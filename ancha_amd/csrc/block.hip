@@ -6,8 +6,9 @@
 // (zero-padded to a multiple of 128 columns, gate bias in the packed bias); `Transformer::load`
 // (:381-409) folds the feed-forward norm into ff_in; `Transformer::forward_kernels` (:464-520)
 // runs packed GEMM (RoPE epilogue) -> gated attention -> out GEMM (+x) -> ff_in GEMM (bias,
-// GELU) -> ff_out GEMM (bias, +x) -> optional output norm. Here the two unit_norm calls are
-// fused into the GEMMs that consume them (ancha_hip_norm_linear).
+// GELU) -> ff_out GEMM (bias, +x) -> optional output norm. Here each unit_norm writes the fp16
+// row its GEMM rounds its operand to (norm_half), and the packed projection, the attention
+// output and the feed-forward hidden activation stay fp16.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
@@ -73,7 +74,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) ==
 int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, size_t m,
          const float* bias, bool gelu, const float* rope, size_t tokens, size_t token_div,
          size_t width, const float* residual, void* out, bool out_half, bool norm,
-         hipStream_t stream) {
+         hipStream_t stream, float q_scale = 0.0f) {
   ancha::Gemm16Params p{};
   p.x = x;
   p.wt = wt;
@@ -92,18 +93,22 @@ int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, siz
   p.norm = norm;
   p.x_half = x_half;
   p.out_half = out_half;
+  p.q_scale = q_scale;
   const hipError_t e = ancha::launch_gemm16(p, stream);
   return e == hipSuccess ? 0 : -static_cast<int>(e);
 }
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
+constexpr float kLog2eHost = 1.4426950408889634f;
+
 }  // namespace
 
-// Workspace regions: the packed projection (fp32 [rows, columns]; later the fp16 FF hidden
-// activation [rows, hidden]), the fp16 attention output [rows, inner], x + attention (fp32).
+// Workspace regions: the packed projection (fp16 [rows, columns]; later the fp16 FF hidden
+// activation [rows, hidden]), the fp16 attention output [rows, inner], x + attention (fp32),
+// the fp16 normalised GEMM operand [rows, dim].
 static size_t region_packed(const ancha_hip_block* b, size_t rows) {
-  const size_t p = rows * b->columns * 4, h = rows * b->hidden * 2;
+  const size_t p = rows * b->columns * 2, h = rows * b->hidden * 2;
   return round_up(p > h ? p : h, 256);
 }
 
@@ -127,27 +132,34 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
   if (rows > 0x7fffffff || rows * b->columns * 4 >= (size_t(1) << 40))
     return ANCHA_HIP_UNSUPPORTED;
   // Attention addresses one sequence with 32-bit offsets from its first row.
-  if (tokens * (split ? split : 1) * b->columns * 4 >= (size_t(1) << 31))
+  if (tokens * (split ? split : 1) * b->columns * 2 >= (size_t(1) << 31))
     return ANCHA_HIP_UNSUPPORTED;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev != b->device) return ANCHA_HIP_INVALID;
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  float* packed = reinterpret_cast<float*>(ws);                      // [rows, columns] fp32
+  _Float16* packed = reinterpret_cast<_Float16*>(ws);                // [rows, columns] fp16
   _Float16* hidden = reinterpret_cast<_Float16*>(ws);                // [rows, hidden] fp16
   _Float16* attended = reinterpret_cast<_Float16*>(ws + region_packed(b, rows));
   float* x1 = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(attended) +
                                        round_up(rows * b->inner * 2, 256));
+  _Float16* xh = reinterpret_cast<_Float16*>(reinterpret_cast<unsigned char*>(x1) +
+                                             round_up(rows * b->dim * 4, 256));
   const size_t dim = b->dim, inner = b->inner;
-  // packed = unit_norm(x) . [Wq|Wk|Wv|Wg|0] + [0|0|0|bg|0], RoPE on the q / k columns.
-  int rc = gemm(x, false, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
-                split ? split : 1, inner, nullptr, packed, false, true, stream);
+  // xh = fp16(unit_norm(x)); packed = xh . [Wq|Wk|Wv|Wg|0] + [0|0|0|bg|0], RoPE on the q / k
+  // columns, q times log2(e) for the exp2-based softmax.
+  hipError_t e = ancha::launch_norm_half(x, static_cast<int>(rows), static_cast<int>(dim),
+                                         nullptr, nullptr, xh, stream);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  int rc = gemm(xh, true, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
+                split ? split : 1, inner, nullptr, packed, true, false, stream, kLog2eHost);
   if (rc) return rc;
   // attended = softmax(q k^T) v * sigmoid(gate), stored fp16.
   ancha::AttnParams ap{};
-  ap.q = packed;
-  ap.k = packed + inner;
-  ap.v = packed + 2 * inner;
-  ap.gate = packed + 3 * inner;
+  ap.q = reinterpret_cast<const float*>(packed);
+  ap.k = reinterpret_cast<const float*>(packed + inner);
+  ap.v = reinterpret_cast<const float*>(packed + 2 * inner);
+  ap.gate = reinterpret_cast<const float*>(packed + 3 * inner);
+  ap.in_half = 1;
   ap.out = reinterpret_cast<float*>(attended);
   ap.ldq = ap.ldk = ap.ldv = ap.ldg = static_cast<long>(b->columns);
   ap.groups = static_cast<int>(groups);
@@ -165,15 +177,18 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
     ap.gstep = 0;
     ap.tstep = 1;
   }
-  hipError_t e = ancha::launch_attention(ap, true, stream);
+  e = ancha::launch_attention(ap, true, stream);
   if (e != hipSuccess) return -static_cast<int>(e);
   // x1 = x + attended . W_out
   rc = gemm(attended, true, rows, inner, b->out_w, dim, nullptr, false, nullptr, 0, 1, 0, x, x1,
             false, false, stream);
   if (rc) return rc;
-  // hidden = GELU(unit_norm(x1) . W1' + b1), stored fp16.
-  rc = gemm(x1, false, rows, dim, b->ff_in_w, b->hidden, b->ff_in_b, true, nullptr, 0, 1, 0,
-            nullptr, hidden, true, true, stream);
+  // hidden = GELU(fp16(unit_norm(x1)) . W1' + b1), stored fp16.
+  e = ancha::launch_norm_half(x1, static_cast<int>(rows), static_cast<int>(dim), nullptr, nullptr,
+                              xh, stream);
+  if (e != hipSuccess) return -static_cast<int>(e);
+  rc = gemm(xh, true, rows, dim, b->ff_in_w, b->hidden, b->ff_in_b, true, nullptr, 0, 1, 0,
+            nullptr, hidden, true, false, stream);
   if (rc) return rc;
   // out = x1 + hidden . W2 + b2
   rc = gemm(hidden, true, rows, b->hidden, b->ff_out_w, dim, b->ff_out_b, false, nullptr, 0, 1, 0,
@@ -250,7 +265,8 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
 
 size_t ancha_hip_block_workspace(const ancha_hip_block* b, size_t rows) {
   if (!b) return 0;
-  return region_packed(b, rows) + round_up(rows * b->inner * 2, 256) + rows * b->dim * 4;
+  return region_packed(b, rows) + round_up(rows * b->inner * 2, 256) +
+         round_up(rows * b->dim * 4, 256) + rows * b->dim * 2;
 }
 
 int ancha_hip_block_forward(const ancha_hip_block* b, const float* x, size_t groups,

@@ -22,6 +22,32 @@ __device__ __forceinline__ float gelu_erf(float x) {
   return 0.5f * x * (1.0f + erff(x * 0.70710678118654752f));
 }
 
+// erf-GELU for epilogues whose result is rounded to fp16: erfc(z) from Abramowitz & Stegun,
+// Handbook of Mathematical Functions, formula 7.1.26 (Hastings' rational approximation,
+// |error| <= 1.5e-7 in erf), with t = 1 / (1 + p z) and exp(-z^2) on the hardware exp2 and
+// reciprocal. GELU(x) = x - x/2 erfc(x/sqrt2) for x >= 0 and x/2 erfc(-x/sqrt2) below, so the
+// negative tail keeps its relative accuracy.
+__device__ __forceinline__ float gelu_fast(float x) {
+  const float z = fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
+  float poly = fmaf(t, 1.061405429f, -1.453152027f);
+  poly = fmaf(t, poly, 1.421413741f);
+  poly = fmaf(t, poly, -0.284496736f);
+  poly = fmaf(t, poly, 0.254829592f);
+  const float erfc = poly * t * __builtin_amdgcn_exp2f(-z * z * 1.44269504088896341f);
+  return 0.5f * x * (x >= 0.0f ? 2.0f - erfc : erfc);
+}
+
+// tanh as 1 - 2 / (e^{2|x|} + 1) with the sign restored; below |x| = 2^-8 the series
+// x (1 - x^2/3) (the cancellation in the first form would cost relative accuracy there).
+__device__ __forceinline__ float tanh_fast(float x) {
+  const float a = fabsf(x);
+  const float e = __builtin_amdgcn_exp2f(a * 2.88539008177792682f);
+  const float r = 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+  const float small = x * fmaf(x * x, -0.333333333f, 1.0f);
+  return a < 0.00390625f ? small : copysignf(r, x);
+}
+
 // Four consecutive floats at element `col` of a row, zero for elements at or past `limit`
 // (the unaligned path handles each element; the aligned path has limit % 4 == 0).
 template <bool ALIGNED>

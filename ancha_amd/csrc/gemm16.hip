@@ -8,12 +8,15 @@
 // Persistent workgroups (two per CU) walk 128 x 128 output tiles; each XCD takes one
 // contiguous range of tiles, column tiles of a row block next to each other, so a row block of
 // x is read from HBM once and re-read from that XCD's L2. Per tile: 4 waves of 64 x 64 (fp16 x)
-// or 8 waves of 64 x 32 (fp32 x) in MFMA 16x16x32 tiles, K in 64-wide steps through a double-buffered LDS tile, global loads one
-// step ahead in registers. After the last K step the accumulators go to LDS, and the loads of
-// the next tile's first step are issued before the epilogue, so they travel while the epilogue
-// reads the tile back row-wise (bias, GELU, rotary, residual: 512-byte coalesced rows) and
-// stores it. Loads past the end of K or of the rows get an offset outside the buffer: they
-// return 0 without touching memory.
+// or 8 waves of 64 x 32 (fp32 x) in MFMA 16x16x32 tiles, K in 64-wide steps through a
+// double-buffered LDS tile, global loads one step ahead in registers. After the last K step the
+// accumulators go to LDS, and the loads of the next tile's first step are issued before the
+// epilogue, so they travel while the epilogue reads the tile back row-wise (bias, GELU / tanh,
+// rotary, residual: 512-byte coalesced rows) and stores it. (Stores straight from the
+// accumulators, 16 rows x 32-64 bytes per instruction, measured slower.) The epilogue's kind is
+// a template parameter for the combinations the block and the mask estimator use. Loads past
+// the end of K or of the rows get an offset outside the buffer: they return 0 without touching
+// memory.
 #include "buffer.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
@@ -49,9 +52,13 @@ struct WStage {
 // chunks are XOR-swizzled by r & 7 so 16 rows written at one chunk hit distinct banks.
 __device__ __forceinline__ int stage_offset(int r, int c) { return r * 512 + ((c ^ (r & 7)) << 4); }
 
+// Epilogue kinds fixed at compile time (the block's and the mask estimator's products: straight
+// code per row, no flag tests); kEpiRuntime reads the flags of Gemm16Params.
+constexpr int kEpiGelu = 1, kEpiTanh = 2, kEpiRope = 4, kEpiResidual = 8, kEpiRuntime = -1;
+
 // WAVES = 4 (64 x 64 per wave) or 8 (64 x 32 per wave: half the accumulators and staging
 // registers per thread, which the fp32-input variants need to stay within 128 registers).
-template <bool XH, bool OH, bool NORM, int WAVES>
+template <bool XH, bool OH, bool NORM, int WAVES, int EPI>
 __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, int col_tiles,
                                                                int tiles) {
   constexpr int NT = WAVES * 64;
@@ -215,24 +222,32 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
     const int col = c0 + 4 * c4;
     float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
     if (p.bias) bias = *reinterpret_cast<const float4*>(p.bias + bt * p.bias_bstride + col);
-    const bool rot = p.rope && col < 2 * p.width;
+    constexpr bool RT = EPI == kEpiRuntime;
+    const bool gelu = RT ? p.gelu != 0 : (EPI & kEpiGelu) != 0;
+    const bool tanh_act = RT ? p.tanh_act != 0 : (EPI & kEpiTanh) != 0;
+    const bool residual = RT ? p.residual != nullptr : (EPI & kEpiResidual) != 0;
+    const bool rot = (RT ? p.rope != nullptr : (EPI & kEpiRope) != 0) && col < 2 * p.width;
     const int table = col < p.width ? 0 : 2;
+    // Rows past the tile's end are computed too (from zero x rows) and their stores fall
+    // outside the output descriptor, so the loop has no exit test and unrolls.
+#pragma unroll
     for (int i = 0; i < kBM / (NT / 32); i++) {
       const int lrow = erow + (NT / 32) * i;
-      if (lrow >= rows) break;
       const float4 a = *reinterpret_cast<const float4*>(lds + stage_offset(lrow, c4));
       const float inv = NORM ? lds_inv[lrow] : 1.0f;
       float4 v = make_float4(a.x * inv + bias.x, a.y * inv + bias.y, a.z * inv + bias.z,
                              a.w * inv + bias.w);
-      if (p.gelu) v = make_float4(gelu_erf(v.x), gelu_erf(v.y), gelu_erf(v.z), gelu_erf(v.w));
-      if (p.tanh_act) v = make_float4(tanhf(v.x), tanhf(v.y), tanhf(v.z), tanhf(v.w));
+      if (gelu) v = make_float4(gelu_fast(v.x), gelu_fast(v.y), gelu_fast(v.z), gelu_fast(v.w));
+      if (tanh_act) v = make_float4(tanh_fast(v.x), tanh_fast(v.y), tanh_fast(v.z), tanh_fast(v.w));
       if (rot) {
         const int tok = ((r0 + lrow) / p.token_div) % p.tokens;
         const unsigned c = ((unsigned)(table * p.tokens + tok) * 64 + (col & 63)) * 4;
         v = rotate4(v, bload4<true>(roper, c), bload4<true>(roper, c + (unsigned)p.tokens * 256));
+        if (table == 0 && p.q_scale != 0.f)
+          v = make_float4(v.x * p.q_scale, v.y * p.q_scale, v.z * p.q_scale, v.w * p.q_scale);
       }
       const unsigned off = (unsigned)lrow * m + col;
-      if (p.residual) {
+      if (residual) {
         const float4 r = bload4<true>(resr, off * 4);
         v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
       }
@@ -247,11 +262,31 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
   }
 }
 
+template <bool XH, bool OH, bool NORM, int EPI>
+void launch_epi(const Gemm16Params& p, int grid, int col_tiles, int tiles, hipStream_t stream) {
+  constexpr int waves = XH ? 4 : 8;
+  hipLaunchKernelGGL((gemm16_kernel<XH, OH, NORM, waves, EPI>), dim3(grid), dim3(waves * 64), 0,
+                     stream, p, col_tiles, tiles);
+}
+
+// Compile-time epilogues for the combinations the block and the mask estimator run; any other
+// flag set takes the runtime-flag kernel.
 template <bool XH, bool OH, bool NORM>
 void launch(const Gemm16Params& p, int grid, int col_tiles, int tiles, hipStream_t stream) {
-  constexpr int waves = XH ? 4 : 8;
-  hipLaunchKernelGGL((gemm16_kernel<XH, OH, NORM, waves>), dim3(grid), dim3(waves * 64), 0,
-                     stream, p, col_tiles, tiles);
+  const int epi = (p.gelu ? kEpiGelu : 0) | (p.tanh_act ? kEpiTanh : 0) |
+                  (p.rope ? kEpiRope : 0) | (p.residual ? kEpiResidual : 0);
+  if constexpr (!NORM && OH) {
+    if (epi == kEpiGelu) return launch_epi<XH, OH, NORM, kEpiGelu>(p, grid, col_tiles, tiles, stream);
+    if (epi == kEpiTanh) return launch_epi<XH, OH, NORM, kEpiTanh>(p, grid, col_tiles, tiles, stream);
+    if (XH && epi == kEpiRope)
+      return launch_epi<XH, OH, NORM, kEpiRope>(p, grid, col_tiles, tiles, stream);
+  }
+  if constexpr (XH && !NORM && !OH) {
+    if (epi == 0) return launch_epi<XH, OH, NORM, 0>(p, grid, col_tiles, tiles, stream);
+    if (epi == kEpiResidual)
+      return launch_epi<XH, OH, NORM, kEpiResidual>(p, grid, col_tiles, tiles, stream);
+  }
+  launch_epi<XH, OH, NORM, kEpiRuntime>(p, grid, col_tiles, tiles, stream);
 }
 
 // Compute units of the current device (cached per device).

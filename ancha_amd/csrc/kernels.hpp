@@ -22,6 +22,9 @@ struct AttnParams {
   long ldq, ldk, ldv, ldg;
   int groups, tokens, heads;
   int out_half;       // store the output as fp16 (the block's internal activation)
+  // q / k / v / gate are fp16 (ld* in fp16 elements) and q already carries log2(e) with the
+  // softmax scale: the block's packed projection. Gated, rope-free, 16-byte aligned calls only.
+  int in_half;
   int gsplit;
   long gouter, gstep, tstep;
 };
@@ -64,6 +67,12 @@ struct NormParams {
 
 hipError_t launch_unit_norm(const NormParams& p, bool aligned, hipStream_t stream);
 
+// Normalised fp16 operand of the block GEMMs (norm.hip), x [rows, dim] contiguous fp32,
+// 16-byte aligned, dim % 4 == 0: y = scale ? unit_norm(x) * scale : x (written to y when y is
+// not null; y may alias x only for dim <= 512), h = fp16(unit_norm(y)) [rows, dim].
+hipError_t launch_norm_half(const float* x, int rows, int dim, const float* scale, float* y,
+                            _Float16* h, hipStream_t stream);
+
 // The block's projection GEMM on load-time fp16 weights: out = epilogue(x . W) with W^T fp16
 // [m][k] (k contiguous, the PyTorch [out, in] layout), x fp32 or fp16 (x_half) [n][k] with row
 // stride ldx, out fp32 or fp16 (out_half) [n][m] contiguous; bias, rope, residual (fp32) and
@@ -81,6 +90,7 @@ struct Gemm16Params {
   int token_div;  // rotary position of row r: (r / token_div) % tokens
   int gelu, norm, x_half, out_half;
   int tanh_act;   // tanh after the bias (the mask estimator's hidden layers)
+  float q_scale;  // factor on the rotated query columns [0, width) (0: none)
   // Batched products (batch > 1): product b reads x + b*x_bstride, wt + b*w_bstride,
   // bias + b*bias_bstride and writes out (and reads residual) at + b*out_bstride (elements).
   // Rotary epilogues are for unbatched calls.
