@@ -118,9 +118,13 @@ static size_t region_packed(const ancha_hip_block* b, size_t rows) {
 // g = b*split + f is rows (b*tokens + t)*split + f: the band pass runs on the time layout, with
 // no transposed copy. Every stage but attention and the rotary epilogue is row-wise, so only
 // those two see the layout. out may be x (x is last read before out is first written).
+// xh_in: the workspace already holds fp16(unit_norm(x)) (the previous block's xh_out).
+// xh_out: the output norm also writes fp16(unit_norm(out)) there for the next block (only with
+// an output norm, dim <= 512 and a next block of the same layout; see block_chainable).
 static int block_forward(const ancha_hip_block* b, const float* x, size_t groups, size_t tokens,
                          size_t split, const float* rope, void* workspace,
-                         size_t workspace_bytes, float* out, hipStream_t stream) {
+                         size_t workspace_bytes, float* out, hipStream_t stream,
+                         bool xh_in = false, bool xh_out = false) {
   if (!b) return ANCHA_HIP_INVALID;
   const size_t rows = groups * tokens;
   if (rows == 0) return ANCHA_HIP_OK;
@@ -147,8 +151,10 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
   const size_t dim = b->dim, inner = b->inner;
   // xh = fp16(unit_norm(x)); packed = xh . [Wq|Wk|Wv|Wg|0] + [0|0|0|bg|0], RoPE on the q / k
   // columns, q times log2(e) for the exp2-based softmax.
-  hipError_t e = ancha::launch_norm_half(x, static_cast<int>(rows), static_cast<int>(dim),
-                                         nullptr, nullptr, xh, stream);
+  hipError_t e = hipSuccess;
+  if (!xh_in)
+    e = ancha::launch_norm_half(x, static_cast<int>(rows), static_cast<int>(dim), nullptr,
+                                nullptr, xh, stream);
   if (e != hipSuccess) return -static_cast<int>(e);
   int rc = gemm(xh, true, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
                 split ? split : 1, inner, nullptr, packed, true, false, stream, kLog2eHost);
@@ -194,9 +200,46 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
   rc = gemm(hidden, true, rows, b->hidden, b->ff_out_w, dim, b->ff_out_b, false, nullptr, 0, 1, 0,
             x1, out, false, false, stream);
   if (rc) return rc;
-  if (b->out_scale) rc = ancha_hip_unit_norm(out, rows, dim, dim, b->out_scale, out, stream);
+  if (b->out_scale && xh_out) {
+    // out = unit_norm(out) * scale in place, and the next block's fp16 operand in one pass.
+    e = ancha::launch_norm_half(out, static_cast<int>(rows), static_cast<int>(dim), b->out_scale,
+                                out, xh, stream);
+    if (e != hipSuccess) return -static_cast<int>(e);
+  } else if (b->out_scale) {
+    rc = ancha_hip_unit_norm(out, rows, dim, dim, b->out_scale, out, stream);
+  }
   return rc;
 }
+
+namespace ancha {
+
+bool block_chainable(const ancha_hip_block* a, const ancha_hip_block* b) {
+  return a && b && a->out_scale && a->dim <= 512 && a->dim == b->dim && a->inner == b->inner &&
+         a->columns == b->columns && a->hidden == b->hidden;
+}
+
+int axis_pair_forward_chained(const ancha_hip_block* time, const ancha_hip_block* band,
+                              const float* x, size_t batch, size_t bands, size_t frames,
+                              const float* time_rope, const float* band_rope, void* workspace,
+                              size_t workspace_bytes, float* out, hipStream_t stream, bool xh_in,
+                              bool xh_out) {
+  if (!time || !band || time->dim != band->dim) return ANCHA_HIP_INVALID;
+  const size_t rows = batch * bands * frames;
+  if (rows == 0) return ANCHA_HIP_OK;
+  if (!x || !out || !time_rope || !band_rope || !workspace) return ANCHA_HIP_INVALID;
+  if (workspace_bytes < ancha_hip_axis_pair_workspace(time, band, rows)) return ANCHA_HIP_INVALID;
+  const bool inner = block_chainable(time, band);
+  // Time pass: groups = batch * bands, sequence = frames, x -> out.
+  int rc = block_forward(time, x, batch * bands, frames, 0, time_rope, workspace, workspace_bytes,
+                         out, stream, xh_in, inner);
+  // Band pass in place on the same [batch, bands, frames, dim] rows: groups = batch * frames,
+  // sequence = bands (network.rs:336-338 transposes instead).
+  if (!rc) rc = block_forward(band, out, batch * frames, bands, frames, band_rope, workspace,
+                              workspace_bytes, out, stream, inner, xh_out);
+  return rc;
+}
+
+}  // namespace ancha
 
 extern "C" {
 
@@ -286,19 +329,9 @@ int ancha_hip_axis_pair_forward(const ancha_hip_block* time, const ancha_hip_blo
                                 const float* x, size_t batch, size_t bands, size_t frames,
                                 const float* time_rope, const float* band_rope, void* workspace,
                                 size_t workspace_bytes, float* out, hipStream_t stream) {
-  if (!time || !band || time->dim != band->dim) return ANCHA_HIP_INVALID;
-  const size_t rows = batch * bands * frames;
-  if (rows == 0) return ANCHA_HIP_OK;
-  if (!x || !out || !time_rope || !band_rope || !workspace) return ANCHA_HIP_INVALID;
-  if (workspace_bytes < ancha_hip_axis_pair_workspace(time, band, rows)) return ANCHA_HIP_INVALID;
-  // Time pass: groups = batch * bands, sequence = frames, x -> out.
-  int rc = block_forward(time, x, batch * bands, frames, 0, time_rope, workspace, workspace_bytes,
-                         out, stream);
-  // Band pass in place on the same [batch, bands, frames, dim] rows: groups = batch * frames,
-  // sequence = bands (network.rs:336-338 transposes instead).
-  if (!rc) rc = block_forward(band, out, batch * frames, bands, frames, band_rope, workspace,
-                              workspace_bytes, out, stream);
-  return rc;
+  return ancha::axis_pair_forward_chained(time, band, x, batch, bands, frames, time_rope,
+                                          band_rope, workspace, workspace_bytes, out, stream,
+                                          false, false);
 }
 
 void ancha_hip_block_destroy(ancha_hip_block* b) {

@@ -3,6 +3,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include "../../include/ancha_hip.h"
+
 namespace ancha {
 
 // softmax(q.k^T).v per (group, head). q/k/v/gate point at the column of head 0 inside
@@ -99,6 +101,17 @@ struct Gemm16Params {
 };
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream);
+
+// Axis pair of two blocks (block.hip) whose output norms hand the next block its fp16 operand:
+// xh_in, the workspace holds fp16(unit_norm(x)) from the previous pair; xh_out, the band block
+// leaves fp16(unit_norm(out)) there for the next pair (which must satisfy block_chainable with
+// it). Between the two blocks of the pair the same hand-over happens when they allow it.
+bool block_chainable(const ancha_hip_block* a, const ancha_hip_block* b);
+int axis_pair_forward_chained(const ancha_hip_block* time, const ancha_hip_block* band,
+                              const float* x, size_t batch, size_t bands, size_t frames,
+                              const float* time_rope, const float* band_rope, void* workspace,
+                              size_t workspace_bytes, float* out, hipStream_t stream, bool xh_in,
+                              bool xh_out);
 
 // Separation runtime (dsp.hip), n_fft = 2048. chunk / audio [2][samples]; spectrum
 // [frames][1025][channel][re, im]; masks [2050][re, im][frames] (one stem); frames_buf

@@ -205,11 +205,16 @@ int forward_impl(ancha_hip_roformer* m, const float* spectrum, size_t frames, vo
   if (e != hipSuccess) return -static_cast<int>(e);
   // Axis loop (network.rs:333-339): x [bands][frames][dim] is the time layout with batch 1.
   const size_t block_bytes = l.total - l.inner;
+  // Each block's output norm also writes the next block's fp16 operand where the blocks allow.
+  bool xh_in = false;
   for (size_t i = 0; i < m->depth; i++) {
-    rc = ancha_hip_axis_pair_forward(m->blocks[2 * i], m->blocks[2 * i + 1], x, 1, m->bands,
-                                     frames, m->time_rope[i], m->band_rope[i], ws + l.inner,
-                                     block_bytes, x, stream);
+    const bool xh_out =
+        i + 1 < m->depth && ancha::block_chainable(m->blocks[2 * i + 1], m->blocks[2 * i + 2]);
+    rc = ancha::axis_pair_forward_chained(m->blocks[2 * i], m->blocks[2 * i + 1], x, 1, m->bands,
+                                          frames, m->time_rope[i], m->band_rope[i], ws + l.inner,
+                                          block_bytes, x, stream, xh_in, xh_out);
     if (rc) return rc;
+    xh_in = xh_out;
   }
   if (m->final_scale) {
     rc = ancha_hip_unit_norm(x, rows, m->dim, m->dim, m->final_scale, x, stream);

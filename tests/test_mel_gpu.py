@@ -74,9 +74,12 @@ def test_istft_round_trip_and_masks(gpu, n, hop):
         assert err < 1e-5 * max(np.abs(want).max(), 1.0)
 
 
-def test_forward_matches_oracle_tiny(gpu):
-    """Two stems, three overlapping bands, 101 frames (time kernel), 3 bands (band kernel)."""
-    config = tiny_config()
+@pytest.mark.parametrize("depth", [1, 3])
+def test_forward_matches_oracle_tiny(gpu, depth):
+    """Two stems, three overlapping bands, 101 frames (time kernel), 3 bands (band kernel).
+    Depth 3 covers the hand-over of each block's output norm to the next block's fp16 operand
+    across layer pairs."""
+    config = tiny_config(depth=depth)
     tensors = W.roformer_tensors(config, seed=31)
     model = S.Roformer(config, tensors, gpu)
     chunk = W.audio(config["chunk_samples"], seed=44)
@@ -85,7 +88,7 @@ def test_forward_matches_oracle_tiny(gpu):
     want = M.model_forward(spec, config, M.weights_from_tensors(config, tensors), threads=8)
     assert got.shape == want.shape == (2, 2050, 2, 101)
     db = snr_db(want, got)
-    report("tiny forward masks SNR dB", db)
+    report(f"tiny forward depth {depth} masks SNR dB", db)
     assert db > 50.0
 
 
