@@ -235,7 +235,6 @@ def layer_cpu_baseline(wt, wb, x, gpu_out, budget_s: float = 12.0) -> dict:
                        f"{len(times)} ({t:.2f} s)")}
 
 
-MEL_CLIP_SECONDS = 30
 
 
 def mel_flops(config: dict) -> float:
@@ -257,14 +256,26 @@ def mel_flops(config: dict) -> float:
     return f + len(config["stems"]) * head
 
 
-def run_mel(args, torch, dev) -> int:
-    """Mel-RoFormer separation (bundled Mel-Karaoke config, random N(0, 0.02) weights) of a
-    30 s stereo clip resident in HBM."""
+SEPARATIONS = {
+    # workload: (bundled config, clip seconds, metric, config description)
+    "mel": ("mel_karaoke", 30, "audio-seconds/sec for Mel-RoFormer fwd",
+            "Mel-RoFormer separation (Mel-Karaoke: 60 bands, dim 384, depth 6, 8x64 heads, "
+            "chunk 352800 / overlap 4) of a 30 s clip"),
+    "bs": ("bs_roformer_large", 300, "audio-seconds/sec for BS-RoFormer-large fwd",
+           "BS-RoFormer-large separation (62 bands, dim 512, depth 12, 8x64 heads, chunk 485100 "
+           "/ overlap 2, chunks one after another) of a 5 min clip"),
+}
+
+
+def run_separation(args, torch, dev) -> int:
+    """Separation of a stereo clip resident in HBM with a bundled config and random
+    N(0, 0.02) weights: Mel-Karaoke on 30 s (`mel`) or BS-RoFormer-large on 5 min (`bs`)."""
     from ancha_amd import separation as S
     from ancha_amd import workload as W
-    config = S.load_config("mel_karaoke")
+    name, seconds, metric, described = SEPARATIONS[args.workload]
+    config = S.load_config(name)
     sr = config["sample_rate"]
-    n = MEL_CLIP_SECONDS * sr
+    n = seconds * sr
     log("generating weights (GPU stream) and the clip")
     tensors = W.roformer_tensors(config, device=dev)
     model = S.Roformer(config, tensors, dev)
@@ -291,18 +302,17 @@ def run_mel(args, torch, dev) -> int:
     chunks = len(range(0, n + 2 * border, step_))
     flops = chunks * mel_flops(config)
     achieved = flops / (gpu_ms * 1e-3) / 1e12
-    log(f"mel separation: {gpu_ms:.1f} ms per {MEL_CLIP_SECONDS} s clip ({chunks} chunks), "
-        f"{MEL_CLIP_SECONDS / (gpu_ms * 1e-3):.1f} audio-s/s, {achieved:.1f} TFLOP/s")
+    log(f"{args.workload} separation: {gpu_ms:.1f} ms per {seconds} s clip ({chunks} chunks), "
+        f"{seconds / (gpu_ms * 1e-3):.1f} audio-s/s, {achieved:.1f} TFLOP/s")
     result = {
-        "metric": "audio-seconds/sec for Mel-RoFormer fwd",
-        "value": round(MEL_CLIP_SECONDS * args.steps / wall, 3),
+        "metric": metric,
+        "value": round(seconds * args.steps / wall, 3),
         "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(wall * 1e3 / args.steps, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
-        "data": "synthetic: seeded pink noise + 3 sines, 30 s stereo 44.1 kHz; weights "
+        "data": f"synthetic: seeded pink noise + 3 sines, {seconds} s stereo 44.1 kHz; weights "
                 "N(0,0.02), gamma 1, rotary theta 10000 (seeded)",
-        "config": {"workload": "Mel-RoFormer separation (Mel-Karaoke: 60 bands, dim 384, depth "
-                               "6, 8x64 heads, chunk 352800 / overlap 4) of a 30 s clip",
+        "config": {"workload": described,
                    "chunks": chunks, "frames_per_chunk": config["chunk_samples"] //
                    config["hop"] + 1, "gflop_per_clip": round(flops / 1e9, 1),
                    "mfma_operands": "fp16", "accumulate": "fp32", "dsp": "fp32",
@@ -314,17 +324,35 @@ def run_mel(args, torch, dev) -> int:
     if not args.no_cpu_baseline:
         import oracle.mel as OM
         threads = cpu_threads()
-        log(f"timing the restated reference CPU path on the first chunk ({threads} threads)")
         weights = OM.weights_from_tensors(config, tensors)
-        t0 = time.perf_counter()
-        OM.separate(audio_np, config, weights, threads=threads, chunks=1)
-        t = time.perf_counter() - t0
-        result["cpu_baseline"] = {
-            "value": round(MEL_CLIP_SECONDS / chunks / t, 5), "unit": "audio-s/s",
-            "cores": threads, "kind": "port",
-            "sample": (f"first of the clip's {chunks} chunks through the full model (STFT, "
-                       f"band split, 6 layer pairs, mask head, iSTFT, overlap-add), "
-                       f"credited {MEL_CLIP_SECONDS}/{chunks} s of audio ({t:.1f} s)")}
+        if args.workload == "mel":
+            log(f"timing the restated reference CPU path on the first chunk ({threads} threads)")
+            t0 = time.perf_counter()
+            OM.separate(audio_np, config, weights, threads=threads, chunks=1)
+            t = time.perf_counter() - t0
+            value = seconds / chunks / t
+            sample = (f"first of the clip's {chunks} chunks through the full model (STFT, "
+                      f"band split, {config['depth']} layer pairs, mask head, iSTFT, "
+                      f"overlap-add), credited {seconds}/{chunks} s of audio ({t:.1f} s)")
+        else:
+            # A whole depth-12 chunk is minutes of CPU work: time the first chunk through a
+            # depth-1 model (same band split, first layer pair, mask head, DSP) and scale the
+            # chunk's CPU time by the FLOP ratio of the full depth.
+            shallow = dict(config, depth=1)
+            weights1 = dict(weights, layers=weights["layers"][:1])
+            log(f"timing the restated reference CPU path: first chunk at depth 1 "
+                f"({threads} threads)")
+            t0 = time.perf_counter()
+            OM.separate(audio_np, shallow, weights1, threads=threads, chunks=1)
+            t = time.perf_counter() - t0
+            full = t * mel_flops(config) / mel_flops(shallow)
+            value = seconds / chunks / full
+            sample = (f"first of the clip's {chunks} chunks through a depth-1 model (band split, "
+                      f"1 layer pair, mask head, STFT / iSTFT) in {t:.1f} s, scaled by the FLOP "
+                      f"ratio {mel_flops(config) / mel_flops(shallow):.2f} to depth "
+                      f"{config['depth']} and credited {seconds}/{chunks} s of audio")
+        result["cpu_baseline"] = {"value": round(value, 5), "unit": "audio-s/s",
+                                  "cores": threads, "kind": "port", "sample": sample}
     del out
     print(json.dumps(result), flush=True)
     return 0
@@ -333,14 +361,20 @@ def run_mel(args, torch, dev) -> int:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", choices=["time", "band", "layer", "mel"], default="time")
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps (default 100; 5 for --workload bs)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed steps (default 10; 1 for --workload bs)")
+    ap.add_argument("--workload", choices=["time", "band", "layer", "mel", "bs"], default="time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain device copy of the workload's I/O size instead; its "
                          "FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic figures")
     args = ap.parse_args()
+    if args.steps is None:
+        args.steps = 5 if args.workload == "bs" else 100
+    if args.warmup is None:
+        args.warmup = 1 if args.workload == "bs" else 10
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(chunk-level data parallelism would need no communication). Run with --gpus 1.",
@@ -359,8 +393,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     if args.workload == "layer":
         return run_layer(args, torch, dev)
-    if args.workload == "mel":
-        return run_mel(args, torch, dev)
+    if args.workload in SEPARATIONS:
+        return run_separation(args, torch, dev)
     shape = W.TIME_SHAPE if args.workload == "time" else W.BAND_SHAPE
     G, T, H, D = shape
     log(f"generating q, k, v {shape} on the GPU")

@@ -126,6 +126,54 @@ def test_separate_matches_oracle_tiny(gpu):
     np.testing.assert_allclose(residual.cpu().numpy(), audio - stems[0].cpu().numpy(), atol=1e-6)
 
 
+def tiny_bs_config(depth=2):
+    """BS-RoFormer at the kernel_package scale: three contiguous bands partitioning the bins, one
+    stem, a final norm instead of per-block output norms, mask MLP counting every Linear in
+    mask_depth (network.rs:138-157)."""
+    config = tiny_config(stems=("vocals",), family="bs-roformer", depth=depth)
+    config["bands"] = [list(range(0, 300)), list(range(300, 700)), list(range(700, 1025))]
+    return config
+
+
+def test_forward_matches_oracle_tiny_bs(gpu):
+    config = tiny_bs_config()
+    tensors = W.roformer_tensors(config, seed=36)
+    model = S.Roformer(config, tensors, gpu)
+    spec = packed_spectrum(W.audio(config["chunk_samples"], seed=48), config["hop"])
+    got = model(torch.from_numpy(spec).to(gpu)).cpu().numpy()
+    want = M.model_forward(spec, config, M.weights_from_tensors(config, tensors), threads=8)
+    assert got.shape == want.shape == (1, 2050, 2, 101)
+    db = snr_db(want, got)
+    report("tiny BS forward masks SNR dB", db)
+    assert db > 50.0
+
+
+def test_separate_matches_oracle_tiny_bs(gpu):
+    config = tiny_bs_config(depth=1)
+    tensors = W.roformer_tensors(config, seed=38)
+    model = S.Roformer(config, tensors, gpu)
+    audio = W.audio(120_000, seed=49)
+    stems, _ = model.separate(torch.from_numpy(audio).to(gpu))
+    want = M.separate(audio, config, M.weights_from_tensors(config, tensors), threads=8)
+    db = snr_db(want[0], stems[0].cpu().numpy())
+    report("tiny BS separation stem SNR dB", db)
+    assert db > 50.0
+
+
+def test_bs_roformer_large_shapes_one_layer_pair(gpu):
+    """The bundled BS-RoFormer-large shapes (62 bands, dim 512, 8 heads, mask MLP x4) at depth 1,
+    on a 101-frame chunk."""
+    config = dict(S.load_config("bs_roformer_large"), depth=1, chunk_samples=44100)
+    tensors = W.roformer_tensors(config, seed=37, device=gpu)
+    model = S.Roformer(config, tensors, gpu)
+    spec = packed_spectrum(W.audio(config["chunk_samples"], seed=47), config["hop"])
+    got = model(torch.from_numpy(spec).to(gpu)).cpu().numpy()
+    want = M.model_forward(spec, config, M.weights_from_tensors(config, tensors), threads=16)
+    db = snr_db(want, got)
+    report("bs-roformer-large depth-1 forward masks SNR dB", db)
+    assert db > 50.0
+
+
 def test_separate_mel_karaoke_one_layer_pair(gpu):
     """The bundled Mel-Karaoke shapes (60 bands, dim 384, 8 heads, 801-frame chunks) at depth 1
     on one chunk."""
