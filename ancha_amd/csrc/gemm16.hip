@@ -73,11 +73,42 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
   // K-step buffers: x tile b at lds + b*kTileBytes, W^T tile b at lds + (2+b)*kTileBytes.
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int n = p.n, k = p.k, m = p.m;
+  const int n = p.n, k = p.k;
   constexpr int xbytes = XH ? 2 : 4;
   const unsigned ldx_b = (unsigned)p.ldx * xbytes, k2 = (unsigned)k * 2;
   const int ktiles = (k + kBK - 1) / kBK;
   const int batch_tiles = ((n + kBM - 1) / kBM) * col_tiles;  // tiles of one product
+  // Tile t -> product, row / column origin, output width, and the product's offsets of W^T
+  // (elements), bias and output.
+  struct TileAt {
+    int bt, r0, c0, m;
+    long wofs, bofs, oofs;
+  };
+  auto decode = [&](int tile) {
+    TileAt d;
+    if (p.group_of_tile) {
+      const int b = p.group_of_tile[tile];
+      const int rt = tile - p.group_first_tile[b], ct = p.group_cols[b] / kBN;
+      const long c0 = p.group_col0[b];
+      d.bt = b;
+      d.r0 = (rt / ct) * kBM;
+      d.c0 = (rt % ct) * kBN;
+      d.m = p.group_cols[b];
+      d.wofs = c0 * k;
+      d.bofs = c0;
+      d.oofs = c0 * n;
+    } else {
+      const int rt = tile % batch_tiles;
+      d.bt = tile / batch_tiles;
+      d.r0 = (rt / col_tiles) * kBM;
+      d.c0 = (rt % col_tiles) * kBN;
+      d.m = p.m;
+      d.wofs = d.bt * p.w_bstride;
+      d.bofs = d.bt * p.bias_bstride;
+      d.oofs = d.bt * p.out_bstride;
+    }
+    return d;
+  };
 
   // Tiles of this workgroup: XCD x (= blockIdx % 8) owns tiles [x*per, (x+1)*per); its
   // workgroups take every (gridDim/8)-th tile of that range.
@@ -96,13 +127,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
   // Loads K step t of tile `tile` (tile >= last: nothing; every load returns 0).
   auto load = [&](int tile, int t) {
     const bool live = tile < last;
-    const int bt = live ? tile / batch_tiles : 0, rt = live ? tile % batch_tiles : 0;
-    const int r0 = live ? (rt / col_tiles) * kBM : 0, c0 = live ? (rt % col_tiles) * kBN : 0;
+    TileAt d{};
+    if (live) d = decode(tile);
+    const int bt = d.bt, r0 = d.r0, c0 = d.c0;
     const int rows = live ? min(kBM, n - r0) : 0;
     const rsrc_t xr = make_rsrc(static_cast<const unsigned char*>(p.x) +
                                     (bt * p.x_bstride + (long)r0 * p.ldx) * xbytes,
                                 rows ? (unsigned)(((long)(rows - 1) * p.ldx + k) * xbytes) : 0u);
-    const rsrc_t wr = make_rsrc(p.wt + bt * p.w_bstride + (long)c0 * k,
+    const rsrc_t wr = make_rsrc(p.wt + d.wofs + (long)c0 * k,
                                 live ? (unsigned)((long)kBN * k * 2) : 0u);
     const int k0 = t * kBK;
     if constexpr (XH) {
@@ -176,8 +208,8 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
 
   load(first, 0);
   for (int tile = first; tile < last; tile += slots) {
-    const int bt = tile / batch_tiles, rt = tile % batch_tiles;
-    const int r0 = (rt / col_tiles) * kBM, c0 = (rt % col_tiles) * kBN;
+    const TileAt d = decode(tile);
+    const int r0 = d.r0, c0 = d.c0, m = d.m;
     const int rows = min(kBM, n - r0);
     if constexpr (NORM)
       for (int i = 0; i < XP; i++) ss[i] = 0.f;
@@ -214,14 +246,14 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
 
     // Row-wise epilogue: bias -> GELU -> rotary -> residual (fused/gemm.rs:46-82 order).
     constexpr int obytes = OH ? 2 : 4;
-    const long orow = bt * p.out_bstride + (long)r0 * m;
+    const long orow = d.oofs + (long)r0 * m;
     const rsrc_t outr = make_rsrc(static_cast<unsigned char*>(p.out) + orow * obytes,
                                   (unsigned)((long)rows * m * obytes));
     const rsrc_t resr = make_rsrc(p.residual ? static_cast<const void*>(p.residual + orow) : any,
                                   p.residual ? (unsigned)((long)rows * m * 4) : 0u);
     const int col = c0 + 4 * c4;
     float4 bias = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (p.bias) bias = *reinterpret_cast<const float4*>(p.bias + bt * p.bias_bstride + col);
+    if (p.bias) bias = *reinterpret_cast<const float4*>(p.bias + d.bofs + col);
     constexpr bool RT = EPI == kEpiRuntime;
     const bool gelu = RT ? p.gelu != 0 : (EPI & kEpiGelu) != 0;
     const bool tanh_act = RT ? p.tanh_act != 0 : (EPI & kEpiTanh) != 0;
@@ -308,7 +340,8 @@ int device_cus() {
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream) {
   const int row_tiles = (p.n + kBM - 1) / kBM, col_tiles = p.m / kBN;
-  const int tiles = row_tiles * col_tiles * (p.batch > 1 ? p.batch : 1);
+  const int tiles = p.group_of_tile ? p.group_tiles
+                                    : row_tiles * col_tiles * (p.batch > 1 ? p.batch : 1);
   // Resident workgroups only (two 4-wave ones per CU for fp16 x; one 8-wave one for fp32 x,
   // whose registers allow three waves per SIMD), a multiple of the XCD count, no more than the
   // tiles need.

@@ -98,6 +98,16 @@ struct Gemm16Params {
   // Rotary epilogues are for unbatched calls.
   int batch;
   long x_bstride, w_bstride, bias_bstride, out_bstride;
+  // Grouped products (group_of_tile not null; batch products, group_tiles tiles in all): tile t
+  // belongs to product b = group_of_tile[t], whose tiles start at group_first_tile[b]; product b
+  // reads x + b*x_bstride and W^T rows from group_col0[b] on, its output is [n][group_cols[b]]
+  // at element group_col0[b]*n, its bias starts at element group_col0[b] (group_cols[b] a
+  // multiple of 128; w_bstride, bias_bstride and out_bstride are not used).
+  const int* group_of_tile;
+  const int* group_first_tile;
+  const int* group_cols;
+  const long* group_col0;
+  int group_tiles;
 };
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream);

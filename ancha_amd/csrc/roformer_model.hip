@@ -79,10 +79,6 @@ struct ancha_hip_roformer {
     float* ob = nullptr;
   };
   std::vector<Head> mask_heads;
-  struct Class {
-    size_t b0, b1, m_pad;
-  };
-  std::vector<Class> classes;
   std::vector<size_t> mpad, colprefix;  // per band padded output width, prefix (columns)
   long* d_band_base = nullptr;
   int *d_band_stride = nullptr, *d_band_width = nullptr;
@@ -90,6 +86,12 @@ struct ancha_hip_roformer {
   // Rotary tables [4][tokens][64] per block, for the frame count they were built for.
   size_t rope_frames = 0;
   std::vector<float*> time_rope, band_rope;
+  // The value|gate projections of all bands as one grouped product: per band output width and
+  // first column; per frame count, the band of each tile and each band's first tile.
+  int* d_group_cols = nullptr;
+  long* d_group_col0 = nullptr;
+  int *d_group_of_tile = nullptr, *d_group_first = nullptr;
+  int group_tiles = 0;
 };
 
 namespace {
@@ -101,7 +103,9 @@ void free_all(ancha_hip_roformer* m) {
                   static_cast<void*>(m->split_b), static_cast<void*>(m->final_scale),
                   static_cast<void*>(m->d_band_base), static_cast<void*>(m->d_band_stride),
                   static_cast<void*>(m->d_band_width), static_cast<void*>(m->d_cover_start),
-                  static_cast<void*>(m->d_cover_band), static_cast<void*>(m->d_cover_local)})
+                  static_cast<void*>(m->d_cover_band), static_cast<void*>(m->d_cover_local),
+                  static_cast<void*>(m->d_group_cols), static_cast<void*>(m->d_group_col0),
+                  static_cast<void*>(m->d_group_of_tile), static_cast<void*>(m->d_group_first)})
     if (p) (void)hipFree(p);
   for (auto* b : m->blocks) ancha_hip_block_destroy(b);
   for (auto& h : m->mask_heads) {
@@ -148,6 +152,9 @@ int ensure_rope(ancha_hip_roformer* m, size_t frames) {
   if (m->rope_frames == frames) return 0;
   for (auto* p : m->time_rope) (void)hipFree(p);
   for (auto* p : m->band_rope) (void)hipFree(p);
+  for (int* p : {m->d_group_of_tile, m->d_group_first})
+    if (p) (void)hipFree(p);
+  m->d_group_of_tile = m->d_group_first = nullptr;
   m->time_rope.assign(m->depth, nullptr);
   m->band_rope.assign(m->depth, nullptr);
   m->rope_frames = 0;
@@ -156,6 +163,18 @@ int ensure_rope(ancha_hip_roformer* m, size_t frames) {
     if (!rc) rc = upload(axis_rope(m->freqs[2 * i + 1], m->bands), &m->band_rope[i]);
     if (rc) return rc;
   }
+  // Tiles of the grouped value|gate product: band b has row tiles x (mpad[b] / 128) of them.
+  const size_t row_tiles = (frames + 127) / 128;
+  std::vector<int> of_tile, first(m->bands);
+  for (size_t b = 0; b < m->bands; b++) {
+    first[b] = static_cast<int>(of_tile.size());
+    of_tile.insert(of_tile.end(), row_tiles * (m->mpad[b] / 128), static_cast<int>(b));
+  }
+  if (of_tile.size() > 0x7fffffff) return ANCHA_HIP_UNSUPPORTED;
+  int rc = upload(of_tile, &m->d_group_of_tile);
+  if (!rc) rc = upload(first, &m->d_group_first);
+  if (rc) return rc;
+  m->group_tiles = static_cast<int>(of_tile.size());
   m->rope_frames = frames;
   return 0;
 }
@@ -239,15 +258,30 @@ int forward_impl(ancha_hip_roformer* m, const float* spectrum, size_t frames, vo
       in_half = true;
       in_dim = mh;
     }
-    // Output projection, value and gate halves side by side, one batched product per run of
-    // bands with the same padded width.
-    for (const auto& c : m->classes) {
-      rc = gemm(static_cast<const _Float16*>(in) + c.b0 * frames * mh, true, frames, mh,
-                head.ow + m->colprefix[c.b0] * mh, c.m_pad, head.ob + m->colprefix[c.b0], false,
-                glu + m->colprefix[c.b0] * frames, false, c.b1 - c.b0,
-                static_cast<long>(frames * mh), static_cast<long>(c.m_pad * mh),
-                static_cast<long>(c.m_pad), static_cast<long>(frames * c.m_pad), stream);
-      if (rc) return rc;
+    // Output projection, value and gate halves side by side: one grouped product over the
+    // bands (band b: [frames, mh] x [mh, mpad[b]] into glu + colprefix[b] * frames).
+    {
+      ancha::Gemm16Params gp16{};
+      gp16.x = in;
+      gp16.wt = head.ow;
+      gp16.bias = head.ob;
+      gp16.out = glu;
+      gp16.ldx = static_cast<long>(mh);
+      gp16.n = static_cast<int>(frames);
+      gp16.k = static_cast<int>(mh);
+      gp16.m = 128;
+      gp16.tokens = 1;
+      gp16.token_div = 1;
+      gp16.x_half = 1;
+      gp16.batch = static_cast<int>(m->bands);
+      gp16.x_bstride = static_cast<long>(frames * mh);
+      gp16.group_of_tile = m->d_group_of_tile;
+      gp16.group_first_tile = m->d_group_first;
+      gp16.group_cols = m->d_group_cols;
+      gp16.group_col0 = m->d_group_col0;
+      gp16.group_tiles = m->group_tiles;
+      e = ancha::launch_gemm16(gp16, stream);
+      if (e != hipSuccess) return -static_cast<int>(e);
     }
     ancha::GluParams gp{};
     gp.glu = glu;
@@ -435,16 +469,23 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
     rc = upload(s, &m->final_scale);
     if (rc) return fail(rc);
   }
-  // Output classes: runs of bands whose value|gate width pads to the same multiple of 128.
+  // Value|gate output width of each band, padded to a multiple of 128, and its first column.
   m->mpad.resize(c->bands);
   m->colprefix.assign(c->bands + 1, 0);
   for (size_t b = 0; b < c->bands; b++) {
     m->mpad[b] = round_up(2 * m->widths[b], 128);
     m->colprefix[b + 1] = m->colprefix[b] + m->mpad[b];
-    if (b == 0 || m->mpad[b] != m->classes.back().m_pad)
-      m->classes.push_back({b, b + 1, m->mpad[b]});
-    else
-      m->classes.back().b1 = b + 1;
+  }
+  {
+    std::vector<int> cols(c->bands);
+    std::vector<long> col0(c->bands);
+    for (size_t b = 0; b < c->bands; b++) {
+      cols[b] = static_cast<int>(m->mpad[b]);
+      col0[b] = static_cast<long>(m->colprefix[b]);
+    }
+    rc = upload(cols, &m->d_group_cols);
+    if (!rc) rc = upload(col0, &m->d_group_col0);
+    if (rc) return fail(rc);
   }
   // Mask heads (network.rs:143-177): hidden layers [bands][out][in] fp16, output [m_pad][mh].
   for (size_t s = 0; s < c->stems; s++) {
