@@ -250,3 +250,32 @@ def test_axis_pair_layer_pair_shape(gpu):
     err = float(np.abs(got - want).max())
     print(f"layer pair band pass on sampled frames: max|diff| {err:.3e}", flush=True)
     assert err < 2e-3
+
+
+@pytest.mark.parametrize("tokens", [1, 2, 17, 63, 64, 65, 127, 128, 129, 200])
+def test_block_ragged_sequence_lengths(gpu, tokens):
+    """The block (fp16 normalised operands, fp16 packed projection read by the attention kernels)
+    at sequence lengths around the band kernel's limit (64) and the time kernel's 64-key tiles,
+    with an output norm; 3 sequences each."""
+    dim, heads, hidden, groups = C.LAYER_DIM, C.LAYER_HEADS, C.LAYER_HIDDEN, 3
+    w = _block_weights(dim, heads, hidden, normalized=True)
+    x = W.normal((groups, tokens, dim), 60 + tokens, 1.0)
+    block = roformer.Transformer(w, gpu)
+    got = block(dev(x, gpu), roformer.axis_rope(w["freqs"], tokens, gpu)).cpu().numpy()
+    want = O.transformer_forward(w, x, kernels=True)
+    err = float(np.abs(got - want).max())
+    print(f"block T={tokens}: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
+
+
+def test_block_wide_rows(gpu):
+    """dim 640 (> 512): the fp16 operand kernel's multi-pass row path."""
+    dim, heads, hidden, groups, tokens = 640, 4, 1280, 2, 70
+    w = _block_weights(dim, heads, hidden, normalized=True)
+    x = W.normal((groups, tokens, dim), 71, 1.0)
+    block = roformer.Transformer(w, gpu)
+    got = block(dev(x, gpu), roformer.axis_rope(W.rope_freqs(), tokens, gpu)).cpu().numpy()
+    want = O.transformer_forward(w, x, kernels=True)
+    err = float(np.abs(got - want).max())
+    print(f"block dim {dim}: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
