@@ -122,10 +122,11 @@ def load_tensors(package: str, manifest: dict) -> dict:
     return out
 
 
-def load_model(package: str, device=None):
-    """Roformer::load (network.rs:79-88): manifest, checked tensors, the GPU model."""
+def load_model(package: str, device=None, plan=None):
+    """Roformer::load (network.rs:79-88): manifest, checked tensors, the GPU model run with
+    ``plan`` (an ``AttentionPlan``; default the GPU backend's)."""
     from .separation import Roformer
 
     manifest = read_manifest(package)
     tensors = load_tensors(package, manifest)
-    return Roformer(manifest["config"], tensors, device), manifest
+    return Roformer(manifest["config"], tensors, device, plan), manifest

@@ -17,6 +17,7 @@ import numpy as np
 import torch
 
 from . import _native
+from .plan import AttentionPlan, backend_plan, require_gpu_kernels, run_settings
 
 N_FFT = 2048
 BINS = N_FFT // 2 + 1
@@ -47,9 +48,14 @@ def _stream(device) -> int:
 
 class Roformer:
     """``Roformer::load`` + ``forward`` (network.rs:79-400) and the chunked ``separate`` of
-    runtime.rs on one device. ``tensors`` maps checkpoint names to float32 arrays."""
+    runtime.rs on one device. ``tensors`` maps checkpoint names to float32 arrays; ``plan``
+    (default: the GPU backend's, backend.rs:52-67) must select the fused attention and custom
+    GEMM kernels."""
 
-    def __init__(self, config: dict, tensors: dict, device: Optional[torch.device] = None):
+    def __init__(self, config: dict, tensors: dict, device: Optional[torch.device] = None,
+                 plan: Optional[AttentionPlan] = None):
+        self.plan = backend_plan("hip") if plan is None else plan
+        require_gpu_kernels(self.plan)
         self.config = dict(config)
         self.device = torch.device(device or "cuda")
         bands = config["bands"]
@@ -89,6 +95,10 @@ class Roformer:
             raise ValueError("model shapes are outside what the kernels cover")
         self._handle = handle
         self._ws: Optional[torch.Tensor] = None
+
+    def settings(self, max_score_mib: int = 512) -> dict:
+        """The plan-derived run-report fields of this model (runtime.rs:62-81, :310-330)."""
+        return run_settings(self.plan, self.config, max_score_mib)
 
     def _workspace(self, need: int) -> torch.Tensor:
         if self._ws is None or self._ws.numel() < need:

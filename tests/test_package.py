@@ -152,6 +152,8 @@ def test_kernel_package_loads_and_matches_oracle(tmp_path):
     config = tiny_package_config(kernel=True)
     tensors = write_package(str(tmp_path), config)
     model, manifest = P.load_model(str(tmp_path), torch.device("cuda:0"))
+    settings = model.settings()
+    assert (settings["attention_kernel"], settings["gemm_kernel"]) == ("fused", "custom")
     chunk = W.audio(config["chunk_samples"], seed=51)
     spec = M.pack_spectra([M.stft(chunk[c], 2048, config["hop"]) for c in range(2)])
     got = model(torch.from_numpy(spec).cuda()).cpu().numpy()
