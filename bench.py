@@ -366,6 +366,9 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=None,
                     help="untimed steps (default 10; 1 for --workload bs)")
     ap.add_argument("--workload", choices=["time", "band", "layer", "mel", "bs"], default="time")
+    ap.add_argument("--tokens", type=int, default=None,
+                    help="sequence length of the time / band op workloads (default 801 / 60); "
+                         "for length sweeps, the headline uses the default")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain device copy of the workload's I/O size instead; its "
@@ -396,7 +399,13 @@ def main() -> int:
     if args.workload in SEPARATIONS:
         return run_separation(args, torch, dev)
     shape = W.TIME_SHAPE if args.workload == "time" else W.BAND_SHAPE
+    if args.tokens is not None:
+        if not 1 <= args.tokens <= 8192:
+            print("--tokens must be in [1, 8192]", file=sys.stderr)
+            return 2
+        shape = (shape[0], args.tokens, shape[2], shape[3])
     G, T, H, D = shape
+    default_shape = args.tokens is None
     log(f"generating q, k, v {shape} on the GPU")
     q, k, v = (W.normal_torch(shape, s, 1.0 / 8.0, device=dev) for s in (1, 2, 3))
     if args.copy_calibration:
@@ -432,12 +441,12 @@ def main() -> int:
         achieved = flops / (kernel_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
-                    "traffic": profiled_traffic("time")}
+                    "traffic": profiled_traffic("time") if default_shape else None}
     else:
         achieved = io_bytes / (kernel_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": profiled_traffic("band")}
+                    "traffic": profiled_traffic("band") if default_shape else None}
     result = {
         "metric": "fused attn TFLOP/s (% MFMA peak)",
         "value": round(value, 3),
