@@ -70,6 +70,7 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
   static_assert(4 * kTileBytes == kStageFloats * 4, "staging tile must fit the LDS pool");
   __shared__ __attribute__((aligned(16))) unsigned char lds[4 * kTileBytes];
   __shared__ float lds_inv[kBM];
+  __shared__ int lds_tok[kBM];
   // K-step buffers: x tile b at lds + b*kTileBytes, W^T tile b at lds + (2+b)*kTileBytes.
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -237,6 +238,9 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
         if ((XH ? c8 : x4) == 0) lds_inv[row] = 1.0f / fmaxf(sqrtf(s), 1e-12f);
       }
     }
+    // Token index of each tile row for the rotary epilogue (read after the barrier below).
+    if ((EPI == kEpiRuntime ? p.rope != nullptr : (EPI & kEpiRope) != 0) && tid < kBM)
+      lds_tok[tid] = ((r0 + tid) / p.token_div) % p.tokens;
     // Accumulators -> LDS (the K-step buffers are free after the barrier above).
     for (int rb = 0; rb < 4; rb++)
       for (int cb = 0; cb < CB; cb++)
@@ -258,13 +262,37 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
     const bool gelu = RT ? p.gelu != 0 : (EPI & kEpiGelu) != 0;
     const bool tanh_act = RT ? p.tanh_act != 0 : (EPI & kEpiTanh) != 0;
     const bool residual = RT ? p.residual != nullptr : (EPI & kEpiResidual) != 0;
-    const bool rot = (RT ? p.rope != nullptr : (EPI & kEpiRope) != 0) && col < 2 * p.width;
+    const bool rope_any = RT ? p.rope != nullptr : (EPI & kEpiRope) != 0;
+    const bool rot = rope_any && col < 2 * p.width;
     const int table = col < p.width ? 0 : 2;
+    // Global inputs of one row (rotary table rows, residual), fetched one row ahead: the wait
+    // for a row's inputs then never covers the stores of the rows before it (the vector
+    // memory counter retires in order).
+    struct RowIn {
+      float4 c, s, r;
+    };
+    // The table rows are read for every column of a rotary product (rows of the v / gate
+    // columns go unused), so the loads sit outside the per-lane rotation test.
+    auto fetch = [&](int i) {
+      const int lrow = erow + (NT / 32) * i;
+      RowIn in;
+      if (rope_any) {
+        const unsigned c = ((unsigned)(table * p.tokens + lds_tok[lrow]) * 64 + (col & 63)) * 4;
+        in.c = bload4<true>(roper, c);
+        in.s = bload4<true>(roper, c + (unsigned)p.tokens * 256);
+      }
+      if (residual) in.r = bload4<true>(resr, ((unsigned)lrow * m + col) * 4);
+      return in;
+    };
+    constexpr int kRows = kBM / (NT / 32);
+    RowIn cur = fetch(0);
     // Rows past the tile's end are computed too (from zero x rows) and their stores fall
     // outside the output descriptor, so the loop has no exit test and unrolls.
 #pragma unroll
-    for (int i = 0; i < kBM / (NT / 32); i++) {
+    for (int i = 0; i < kRows; i++) {
       const int lrow = erow + (NT / 32) * i;
+      const RowIn in = cur;
+      if (i + 1 < kRows) cur = fetch(i + 1);
       const float4 a = *reinterpret_cast<const float4*>(lds + stage_offset(lrow, c4));
       const float inv = NORM ? lds_inv[lrow] : 1.0f;
       float4 v = make_float4(a.x * inv + bias.x, a.y * inv + bias.y, a.z * inv + bias.z,
@@ -272,17 +300,12 @@ __global__ __launch_bounds__(WAVES * 64, 2) void gemm16_kernel(Gemm16Params p, i
       if (gelu) v = make_float4(gelu_fast(v.x), gelu_fast(v.y), gelu_fast(v.z), gelu_fast(v.w));
       if (tanh_act) v = make_float4(tanh_fast(v.x), tanh_fast(v.y), tanh_fast(v.z), tanh_fast(v.w));
       if (rot) {
-        const int tok = ((r0 + lrow) / p.token_div) % p.tokens;
-        const unsigned c = ((unsigned)(table * p.tokens + tok) * 64 + (col & 63)) * 4;
-        v = rotate4(v, bload4<true>(roper, c), bload4<true>(roper, c + (unsigned)p.tokens * 256));
+        v = rotate4(v, in.c, in.s);
         if (table == 0 && p.q_scale != 0.f)
           v = make_float4(v.x * p.q_scale, v.y * p.q_scale, v.z * p.q_scale, v.w * p.q_scale);
       }
       const unsigned off = (unsigned)lrow * m + col;
-      if (residual) {
-        const float4 r = bload4<true>(resr, off * 4);
-        v = make_float4(v.x + r.x, v.y + r.y, v.z + r.z, v.w + r.w);
-      }
+      if (residual) v = make_float4(v.x + in.r.x, v.y + in.r.y, v.z + in.r.z, v.w + in.r.w);
       if constexpr (OH) {
         const u32x2 h = {pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
         __builtin_amdgcn_raw_buffer_store_b64(h, outr, off * 2, 0, 0);
