@@ -27,15 +27,18 @@ __device__ __forceinline__ float gelu_erf(float x) {
 // |error| <= 1.5e-7 in erf), with t = 1 / (1 + p z) and exp(-z^2) on the hardware exp2 and
 // reciprocal. GELU(x) = x - x/2 erfc(x/sqrt2) for x >= 0 and x/2 erfc(-x/sqrt2) below, so the
 // negative tail keeps its relative accuracy.
+// The constants are folded for the VALU: p / sqrt2 multiplies |x| directly, the polynomial
+// carries the factor 1/2 (so h = x erfc(|x|/sqrt2) / 2 is three multiplies), and
+// exp(-z^2) = exp2(x^2 * (-log2(e) / 2)).
 __device__ __forceinline__ float gelu_fast(float x) {
-  const float z = fabsf(x) * 0.70710678118654752f;
-  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f, z, 1.0f));
-  float poly = fmaf(t, 1.061405429f, -1.453152027f);
-  poly = fmaf(t, poly, 1.421413741f);
-  poly = fmaf(t, poly, -0.284496736f);
-  poly = fmaf(t, poly, 0.254829592f);
-  const float erfc = poly * t * __builtin_amdgcn_exp2f(-z * z * 1.44269504088896341f);
-  return 0.5f * x * (x >= 0.0f ? 2.0f - erfc : erfc);
+  const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, fabsf(x), 1.0f));
+  float poly = fmaf(t, 0.5f * 1.061405429f, 0.5f * -1.453152027f);
+  poly = fmaf(t, poly, 0.5f * 1.421413741f);
+  poly = fmaf(t, poly, 0.5f * -0.284496736f);
+  poly = fmaf(t, poly, 0.5f * 0.254829592f);
+  const float e = __builtin_amdgcn_exp2f(x * -0.72134752044448170f * x);
+  const float h = x * (poly * t * e);
+  return x >= 0.0f ? x - h : h;
 }
 
 // tanh as 1 - 2 / (e^{2|x|} + 1) with the sign restored; below |x| = 2^-8 the series
