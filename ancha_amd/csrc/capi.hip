@@ -2,6 +2,7 @@
 // dispatch to the gfx950 kernels.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdint>
 #include <cstdio>
@@ -65,10 +66,17 @@ constexpr size_t kIntMax = 0x7fffffff;
 int run_attention(ancha::AttnParams& p, size_t groups, size_t tokens, size_t heads,
                   hipStream_t stream, const char* name) {
   if (groups == 0 || tokens == 0 || heads == 0) return ANCHA_HIP_OK;
-  if (!device_is_gfx950()) return fail(ANCHA_HIP_UNSUPPORTED, std::string(name) + ": not a gfx950 device");
   const size_t qblocks = (tokens + 127) / 128;
   if (tokens > kIntMax || groups * heads > kIntMax || groups * heads * qblocks > kIntMax)
     return fail(ANCHA_HIP_UNSUPPORTED, std::string(name) + ": problem count exceeds the grid");
+  // The kernels address one (group, head) sequence through 32-bit buffer ranges of
+  // (tokens - 1) rows of stride plus one row, in bytes.
+  const size_t ld = std::max({static_cast<size_t>(p.ldq), static_cast<size_t>(p.ldk),
+                              static_cast<size_t>(p.ldv), static_cast<size_t>(p.ldg),
+                              heads * kHeadDim});
+  if (tokens > 1 && ld > (0xffffffffull - kHeadDim * 4) / 4 / (tokens - 1))
+    return fail(ANCHA_HIP_UNSUPPORTED, std::string(name) + ": rows exceed the 32-bit buffer range");
+  if (!device_is_gfx950()) return fail(ANCHA_HIP_UNSUPPORTED, std::string(name) + ": not a gfx950 device");
   p.groups = static_cast<int>(groups);
   p.tokens = static_cast<int>(tokens);
   p.heads = static_cast<int>(heads);

@@ -41,6 +41,10 @@ def test_argument_checks_without_a_device(lib):
     assert lib.ancha_hip_attention(None, p, p, 1, 4, 1, 64, 64, 64, None, p, None) == _native.INVALID
     # Packed projection narrower than heads*(3*64+1) -> UNSUPPORTED (the reference's None).
     assert lib.ancha_hip_gated_attention(p, 1, 4, 3 * 64, 1, None, p, None) == _native.UNSUPPORTED
+    # Sequences whose rows span more than a 32-bit buffer range -> UNSUPPORTED (checked before
+    # any device query; the pointers are never read on the host).
+    rc = lib.ancha_hip_attention(p, p, p, 1, 1 << 20, 1, 4096, 4096, 4096, None, p, None)
+    assert rc == _native.UNSUPPORTED and "32-bit buffer range" in _native.last_error()
     # Empty problems launch nothing and succeed.
     assert lib.ancha_hip_attention(p, p, p, 0, 4, 1, 64, 64, 64, None, p, None) == _native.OK
     assert lib.ancha_hip_attention(p, p, p, 1, 0, 1, 64, 64, 64, None, p, None) == _native.OK
