@@ -183,13 +183,15 @@ int ensure_rope(ancha_hip_roformer* m, size_t frames) {
 struct Layout {
   size_t x, inner, h1, h2, glu, total;
 };
-Layout forward_layout(const ancha_hip_roformer* m, size_t frames) {
+// nch chunks share the axis loop (x [nch][bands][frames][dim]); the mask heads run one chunk
+// at a time in the same head buffers.
+Layout forward_layout(const ancha_hip_roformer* m, size_t frames, size_t nch = 1) {
   Layout l{};
   const size_t rows = m->bands * frames;
   l.x = 0;
   const size_t block_ws =
-      ancha_hip_axis_pair_workspace(m->blocks[0], m->blocks[1], rows);
-  l.inner = round_up(rows * m->dim * 4, 256);
+      ancha_hip_axis_pair_workspace(m->blocks[0], m->blocks[1], nch * rows);
+  l.inner = round_up(nch * rows * m->dim * 4, 256);
   l.h1 = l.inner;
   l.h2 = l.h1 + round_up(rows * m->mask_hidden * 2, 256);
   l.glu = l.h2 + round_up(rows * m->mask_hidden * 2, 256);
@@ -199,16 +201,16 @@ Layout forward_layout(const ancha_hip_roformer* m, size_t frames) {
   return l;
 }
 
-int forward_impl(ancha_hip_roformer* m, const float* spectrum, size_t frames, void* workspace,
-                 float* masks, hipStream_t stream) {
+// Forward of nch chunks' spectra (1 or 2) into their masks.
+int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch, size_t frames,
+                 void* workspace, float* const* masks_of, hipStream_t stream) {
   unsigned char* ws = static_cast<unsigned char*>(workspace);
-  const Layout l = forward_layout(m, frames);
+  const Layout l = forward_layout(m, frames, nch);
   float* x = reinterpret_cast<float*>(ws + l.x);
   const size_t rows = m->bands * frames;
   int rc = ensure_rope(m, frames);
   if (rc) return rc;
   ancha::BandSplitParams bp{};
-  bp.spectrum = spectrum;
   bp.offsets = m->d_offsets;
   bp.bins = m->d_bins;
   bp.wofs = m->d_wofs;
@@ -220,32 +222,39 @@ int forward_impl(ancha_hip_roformer* m, const float* spectrum, size_t frames, vo
   bp.cols = static_cast<int>(4 * m->fft_bins);
   bp.dim = static_cast<int>(m->dim);
   bp.max_width = static_cast<int>(m->max_width);
-  hipError_t e = ancha::launch_band_split(bp, stream);
+  hipError_t e = hipSuccess;
+  for (size_t c = 0; c < nch && e == hipSuccess; c++) {
+    bp.spectrum = spectra[c];
+    bp.x = x + c * rows * m->dim;
+    e = ancha::launch_band_split(bp, stream);
+  }
   if (e != hipSuccess) return -static_cast<int>(e);
-  // Axis loop (network.rs:333-339): x [bands][frames][dim] is the time layout with batch 1.
+  // Axis loop (network.rs:333-339): x [nch][bands][frames][dim] is the time layout with batch
+  // nch.
   const size_t block_bytes = l.total - l.inner;
   // Each block's output norm also writes the next block's fp16 operand where the blocks allow.
   bool xh_in = false;
   for (size_t i = 0; i < m->depth; i++) {
     const bool xh_out =
         i + 1 < m->depth && ancha::block_chainable(m->blocks[2 * i + 1], m->blocks[2 * i + 2]);
-    rc = ancha::axis_pair_forward_chained(m->blocks[2 * i], m->blocks[2 * i + 1], x, 1, m->bands,
+    rc = ancha::axis_pair_forward_chained(m->blocks[2 * i], m->blocks[2 * i + 1], x, nch, m->bands,
                                           frames, m->time_rope[i], m->band_rope[i], ws + l.inner,
                                           block_bytes, x, stream, xh_in, xh_out);
     if (rc) return rc;
     xh_in = xh_out;
   }
   if (m->final_scale) {
-    rc = ancha_hip_unit_norm(x, rows, m->dim, m->dim, m->final_scale, x, stream);
+    rc = ancha_hip_unit_norm(x, nch * rows, m->dim, m->dim, m->final_scale, x, stream);
     if (rc) return rc;
   }
   _Float16* h[2] = {reinterpret_cast<_Float16*>(ws + l.h1), reinterpret_cast<_Float16*>(ws + l.h2)};
   float* glu = reinterpret_cast<float*>(ws + l.glu);
   const size_t mh = m->mask_hidden;
+  for (size_t c = 0; c < nch; c++)
   for (size_t s = 0; s < m->stems; s++) {
     const ancha_hip_roformer::Head& head = m->mask_heads[s];
     // Hidden layers (network.rs:377-379): h = tanh(W h + b) per band, fp16 between layers.
-    const void* in = x;
+    const void* in = x + c * rows * m->dim;
     bool in_half = false;
     size_t in_dim = m->dim;
     for (size_t layer = 0; layer < m->mask_layers; layer++) {
@@ -291,7 +300,7 @@ int forward_impl(ancha_hip_roformer* m, const float* spectrum, size_t frames, vo
     gp.cover_start = m->d_cover_start;
     gp.cover_band = m->d_cover_band;
     gp.cover_local = m->d_cover_local;
-    gp.masks = masks + s * 4 * m->fft_bins * frames;
+    gp.masks = masks_of[c] + s * 4 * m->fft_bins * frames;
     gp.outputs = static_cast<int>(4 * m->fft_bins);
     gp.frames = static_cast<int>(frames);
     e = ancha::launch_glu_gather(gp, stream);
@@ -328,13 +337,14 @@ SepLayout separate_layout(const ancha_hip_roformer* m, size_t samples) {
     o += round_up(bytes, 256);
     return at;
   };
-  l.chunk = take(2 * m->chunk * 4);
-  l.spectrum = take(p.frames * 4 * m->fft_bins * 4);
-  l.masks = take(m->stems * 4 * m->fft_bins * p.frames * 4);
+  // Two chunks at a time go through the model together.
+  l.chunk = take(2 * 2 * m->chunk * 4);
+  l.spectrum = take(2 * p.frames * 4 * m->fft_bins * 4);
+  l.masks = take(2 * m->stems * 4 * m->fft_bins * p.frames * 4);
   l.frames_buf = take(p.frames * 2 * kFft * 4);
   l.sums = take(m->stems * 2 * p.length * 4);
   l.weights = take(p.length * 4);
-  l.model = take(forward_layout(m, p.frames).total);
+  l.model = take(forward_layout(m, p.frames, p.starts.size() > 1 ? 2 : 1).total);
   l.total = o;
   return l;
 }
@@ -584,7 +594,7 @@ int ancha_hip_roformer_forward(ancha_hip_roformer* m, const float* spectrum, siz
   if (workspace_bytes < ancha_hip_roformer_workspace(m, frames)) return ANCHA_HIP_INVALID;
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev != m->device) return ANCHA_HIP_INVALID;
-  return forward_impl(m, spectrum, frames, workspace, masks, stream);
+  return forward_impl(m, &spectrum, 1, frames, workspace, &masks, stream);
 }
 
 size_t ancha_hip_separate_workspace(const ancha_hip_roformer* m, size_t samples) {
@@ -616,24 +626,41 @@ int ancha_hip_separate(ancha_hip_roformer* m, const float* audio, size_t samples
   if (e == hipSuccess) e = ancha::launch_zero(weights, length, stream);
   if (e != hipSuccess) return -static_cast<int>(e);
   const size_t mask_stride = 4 * m->fft_bins * p.frames;
-  for (size_t start : p.starts) {
-    const long remaining = std::min<long>(length - static_cast<long>(start), cs);
-    e = ancha::launch_chunk_gather(audio, static_cast<long>(samples), static_cast<long>(start),
-                                   static_cast<long>(p.border), remaining, cs, chunk, stream);
-    if (e == hipSuccess) e = ancha::launch_stft(chunk, cs, static_cast<int>(m->hop), spectrum, stream);
-    if (e != hipSuccess) return -static_cast<int>(e);
-    int rc = forward_impl(m, spectrum, p.frames, ws + l.model, masks, stream);
-    if (rc) return rc;
-    const bool first = start == 0, last = static_cast<long>(start) + cs >= length;
-    for (size_t s = 0; s < m->stems; s++) {
-      e = ancha::launch_istft_frames(spectrum, masks + s * mask_stride, static_cast<int>(p.frames),
-                                     m->zero_dc ? 1 : 0, frames_buf, stream);
+  const size_t chunk_floats = 2 * m->chunk, spectrum_floats = p.frames * 4 * m->fft_bins;
+  for (size_t i = 0; i < p.starts.size(); i += 2) {
+    const size_t nch = std::min<size_t>(2, p.starts.size() - i);
+    const float* spectra[2];
+    float* masks_of[2];
+    for (size_t c = 0; c < nch; c++) {
+      const size_t start = p.starts[i + c];
+      const long remaining = std::min<long>(length - static_cast<long>(start), cs);
+      float* chunk_c = chunk + c * chunk_floats;
+      float* spectrum_c = spectrum + c * spectrum_floats;
+      e = ancha::launch_chunk_gather(audio, static_cast<long>(samples), static_cast<long>(start),
+                                     static_cast<long>(p.border), remaining, cs, chunk_c, stream);
       if (e == hipSuccess)
-        e = ancha::launch_ola_accumulate(frames_buf, static_cast<int>(p.frames),
-                                         static_cast<int>(m->hop), cs, static_cast<long>(start),
-                                         length, first, last, s == 0, sums + s * 2 * length,
-                                         weights, stream);
+        e = ancha::launch_stft(chunk_c, cs, static_cast<int>(m->hop), spectrum_c, stream);
       if (e != hipSuccess) return -static_cast<int>(e);
+      spectra[c] = spectrum_c;
+      masks_of[c] = masks + c * m->stems * mask_stride;
+    }
+    int rc = forward_impl(m, spectra, nch, p.frames, ws + l.model, masks_of, stream);
+    if (rc) return rc;
+    // Overlap-add in chunk order, as one chunk at a time would.
+    for (size_t c = 0; c < nch; c++) {
+      const size_t start = p.starts[i + c];
+      const bool first = start == 0, last = static_cast<long>(start) + cs >= length;
+      for (size_t s = 0; s < m->stems; s++) {
+        e = ancha::launch_istft_frames(spectra[c], masks_of[c] + s * mask_stride,
+                                       static_cast<int>(p.frames), m->zero_dc ? 1 : 0,
+                                       frames_buf, stream);
+        if (e == hipSuccess)
+          e = ancha::launch_ola_accumulate(frames_buf, static_cast<int>(p.frames),
+                                           static_cast<int>(m->hop), cs,
+                                           static_cast<long>(start), length, first, last, s == 0,
+                                           sums + s * 2 * length, weights, stream);
+        if (e != hipSuccess) return -static_cast<int>(e);
+      }
     }
   }
   for (size_t s = 0; s < m->stems; s++) {
