@@ -72,6 +72,8 @@ hipError_t launch_unit_norm(const NormParams& p, bool aligned, hipStream_t strea
 // Normalised fp16 operand of the block GEMMs (norm.hip), x [rows, dim] contiguous fp32,
 // 16-byte aligned, dim % 4 == 0: y = scale ? unit_norm(x) * scale : x (written to y when y is
 // not null; y may alias x only for dim <= 512), h = fp16(unit_norm(y)) [rows, dim].
+// h = fp16(x) for n floats (n % 8 == 0, 16-byte aligned), round to nearest even.
+hipError_t launch_cast_half(const float* x, long n, _Float16* h, hipStream_t stream);
 hipError_t launch_norm_half(const float* x, int rows, int dim, const float* scale, float* y,
                             _Float16* h, hipStream_t stream);
 

@@ -138,7 +138,26 @@ __global__ __launch_bounds__(256) void norm_half_kernel(const float* x, int rows
   }
 }
 
+// fp16 copy of n floats, 8 per thread (n % 8 == 0), rounded to nearest even as the GEMMs
+// round their fp32 operands.
+__global__ __launch_bounds__(256) void cast_half_kernel(const float4* x, long n8, u32x4* h) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const float4 a = x[2 * i], b = x[2 * i + 1];
+  h[i] = u32x4{pack_h2(a.x, a.y), pack_h2(a.z, a.w), pack_h2(b.x, b.y), pack_h2(b.z, b.w)};
+}
+
 }  // namespace
+
+hipError_t launch_cast_half(const float* x, long n, _Float16* h, hipStream_t stream) {
+  if (n < 0 || n % 8 || (reinterpret_cast<uintptr_t>(x) & 15) || (reinterpret_cast<uintptr_t>(h) & 15))
+    return hipErrorInvalidValue;
+  if (n == 0) return hipSuccess;
+  const long n8 = n / 8;
+  hipLaunchKernelGGL(cast_half_kernel, dim3((unsigned)((n8 + 255) / 256)), dim3(256), 0, stream,
+                     reinterpret_cast<const float4*>(x), n8, reinterpret_cast<u32x4*>(h));
+  return hipGetLastError();
+}
 
 hipError_t launch_norm_half(const float* x, int rows, int dim, const float* scale, float* y,
                             _Float16* h, hipStream_t stream) {

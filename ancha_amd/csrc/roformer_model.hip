@@ -181,7 +181,7 @@ int ensure_rope(ancha_hip_roformer* m, size_t frames) {
 
 // Workspace regions of a forward over `frames` frames.
 struct Layout {
-  size_t x, inner, h1, h2, glu, total;
+  size_t x, inner, h1, h2, glu, xh, total;
 };
 // nch chunks share the axis loop (x [nch][bands][frames][dim]); the mask heads run one chunk
 // at a time in the same head buffers.
@@ -195,7 +195,9 @@ Layout forward_layout(const ancha_hip_roformer* m, size_t frames, size_t nch = 1
   l.h1 = l.inner;
   l.h2 = l.h1 + round_up(rows * m->mask_hidden * 2, 256);
   l.glu = l.h2 + round_up(rows * m->mask_hidden * 2, 256);
-  const size_t heads_end = l.glu + round_up(frames * m->colprefix.back() * 4, 256);
+  // fp16 copy of x for the first mask layer, past the head buffers.
+  l.xh = l.glu + round_up(frames * m->colprefix.back() * 4, 256);
+  const size_t heads_end = l.xh + round_up(nch * rows * m->dim * 2, 256);
   const size_t blocks_end = l.inner + round_up(block_ws, 256);
   l.total = heads_end > blocks_end ? heads_end : blocks_end;
   return l;
@@ -248,14 +250,22 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
     if (rc) return rc;
   }
   _Float16* h[2] = {reinterpret_cast<_Float16*>(ws + l.h1), reinterpret_cast<_Float16*>(ws + l.h2)};
+  // The first mask layer reads x as fp16, the operand the fp32-input GEMM would round to.
+  _Float16* xh = reinterpret_cast<_Float16*>(ws + l.xh);
+  const bool cast = m->dim % 8 == 0;
+  if (cast) {
+    e = ancha::launch_cast_half(x, static_cast<long>(nch * rows * m->dim), xh, stream);
+    if (e != hipSuccess) return -static_cast<int>(e);
+  }
   float* glu = reinterpret_cast<float*>(ws + l.glu);
   const size_t mh = m->mask_hidden;
   for (size_t c = 0; c < nch; c++)
   for (size_t s = 0; s < m->stems; s++) {
     const ancha_hip_roformer::Head& head = m->mask_heads[s];
     // Hidden layers (network.rs:377-379): h = tanh(W h + b) per band, fp16 between layers.
-    const void* in = x + c * rows * m->dim;
-    bool in_half = false;
+    const void* in = cast ? static_cast<const void*>(xh + c * rows * m->dim)
+                          : static_cast<const void*>(x + c * rows * m->dim);
+    bool in_half = cast;
     size_t in_dim = m->dim;
     for (size_t layer = 0; layer < m->mask_layers; layer++) {
       _Float16* out = h[layer & 1];
