@@ -14,11 +14,15 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "_lib", "libancha_hip.so")
 CSRC = os.path.join(HERE, "csrc")
 
-OK, UNSUPPORTED, INVALID = 0, 1, 2
+OK, UNSUPPORTED, INVALID, CANCELLED = 0, 1, 2, 3
 
 
 class HipError(RuntimeError):
     """A HIP runtime failure (sticky, like the reference's device::check)."""
+
+
+class Cancelled(RuntimeError):
+    """The caller's cancellation flag stopped the call ("task cancelled")."""
 
 
 def build(jobs: int = 8) -> str:
@@ -49,9 +53,9 @@ SIGNATURES = {
     "ancha_hip_axis_pair_forward": (_int, [_p, _p, _p, _sz, _sz, _sz, _p, _p, _p, _sz, _p, _p]),
     "ancha_hip_roformer_create": (_int, [_p, _p, _p, ctypes.POINTER(_p)]),
     "ancha_hip_roformer_workspace": (_sz, [_p, _sz]),
-    "ancha_hip_roformer_forward": (_int, [_p, _p, _sz, _p, _sz, _p, _p]),
+    "ancha_hip_roformer_forward": (_int, [_p, _p, _sz, _p, _sz, _p, _p, _p]),
     "ancha_hip_separate_workspace": (_sz, [_p, _sz]),
-    "ancha_hip_separate": (_int, [_p, _p, _sz, _p, _sz, _p, _p, _p]),
+    "ancha_hip_separate": (_int, [_p, _p, _sz, _p, _sz, _p, _p, _p, _p]),
     "ancha_hip_roformer_destroy": (None, [_p]),
     "ancha_hip_stft": (_int, [_p, _sz, _sz, _p, _p]),
     "ancha_hip_istft_workspace": (_sz, [_sz]),
@@ -93,4 +97,6 @@ def check(rc: int) -> bool:
         return False
     if rc == INVALID:
         raise ValueError(last_error())
+    if rc == CANCELLED:
+        raise Cancelled(last_error())
     raise HipError(f"{last_error()} (code {rc})")

@@ -643,6 +643,15 @@ static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+bool attention_grid_fits(size_t groups, size_t tokens, size_t heads) {
+  const size_t problems = groups * heads;
+  if (groups != 0 && problems / groups != heads) return false;
+  const size_t blocks =
+      tokens <= 64 ? problems : problems * ((tokens + kTimeQueries - 1) / kTimeQueries);
+  const size_t threads = tokens <= 64 ? 256 : kTimeWaves * 64;
+  return blocks < (size_t(1) << 31) && blocks * threads < (size_t(1) << 32);
+}
+
 hipError_t launch_attention(const AttnParams& params, bool aligned, hipStream_t stream) {
   AttnParams p = params;
   if (p.gsplit == 0) {

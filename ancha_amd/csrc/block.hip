@@ -14,11 +14,13 @@
 #include <cmath>
 #include <cstdint>
 #include <cstring>
+#include <string>
 #include <new>
 #include <vector>
 
 #include "../../include/ancha_hip.h"
 #include "kernels.hpp"
+#include "status.hpp"
 
 // Weights are stored as fp16 W^T [out][in] (the PyTorch layout, folded scales applied before
 // rounding): the GEMMs round every operand to fp16 anyway, so converting once at load time
@@ -65,7 +67,7 @@ int upload(const std::vector<T>& host, T** dev) {
   hipError_t e = hipMalloc(reinterpret_cast<void**>(dev), host.size() * sizeof(T));
   if (e == hipSuccess)
     e = hipMemcpy(*dev, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice);
-  return e == hipSuccess ? 0 : -static_cast<int>(e);
+  return ancha::hip_status(e, "ancha_hip_block_create: weight upload");
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -94,8 +96,7 @@ int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, siz
   p.x_half = x_half;
   p.out_half = out_half;
   p.q_scale = q_scale;
-  const hipError_t e = ancha::launch_gemm16(p, stream);
-  return e == hipSuccess ? 0 : -static_cast<int>(e);
+  return ancha::hip_status(ancha::launch_gemm16(p, stream), "block GEMM");
 }
 
 size_t round_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
@@ -125,21 +126,24 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
                          size_t split, const float* rope, void* workspace,
                          size_t workspace_bytes, float* out, hipStream_t stream,
                          bool xh_in = false, bool xh_out = false) {
-  if (!b) return ANCHA_HIP_INVALID;
+  static const std::string kWhere = "ancha_hip_block_forward: ";
+  auto invalid = [](const char* why) { return ancha::fail(ANCHA_HIP_INVALID, kWhere + why); };
+  if (!b) return invalid("null block");
   const size_t rows = groups * tokens;
   if (rows == 0) return ANCHA_HIP_OK;
-  if (!x || !out || !rope || !workspace) return ANCHA_HIP_INVALID;
-  if (workspace_bytes < ancha_hip_block_workspace(b, rows)) return ANCHA_HIP_INVALID;
+  if (!x || !out || !rope || !workspace) return invalid("null buffer");
+  if (workspace_bytes < ancha_hip_block_workspace(b, rows)) return invalid("workspace too small");
   if (!aligned16(x) || !aligned16(out) || !aligned16(rope) || !aligned16(workspace))
-    return ANCHA_HIP_INVALID;
-  if (split && groups % split) return ANCHA_HIP_INVALID;
-  if (rows > 0x7fffffff || rows * b->columns * 4 >= (size_t(1) << 40))
-    return ANCHA_HIP_UNSUPPORTED;
+    return invalid("buffer not 16-byte aligned");
+  if (split && groups % split) return invalid("groups not a multiple of the frame count");
   // Attention addresses one sequence with 32-bit offsets from its first row.
-  if (tokens * (split ? split : 1) * b->columns * 2 >= (size_t(1) << 31))
-    return ANCHA_HIP_UNSUPPORTED;
+  if (rows > 0x7fffffff || rows * b->columns * 4 >= (size_t(1) << 40) ||
+      tokens * (split ? split : 1) * b->columns * 2 >= (size_t(1) << 31) ||
+      !ancha::attention_grid_fits(groups, tokens, b->heads))
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "rows exceed the kernels' ranges");
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev != b->device) return ANCHA_HIP_INVALID;
+  if (hipGetDevice(&dev) != hipSuccess || dev != b->device)
+    return invalid("called on another device than the block's");
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   _Float16* packed = reinterpret_cast<_Float16*>(ws);                // [rows, columns] fp16
   _Float16* hidden = reinterpret_cast<_Float16*>(ws);                // [rows, hidden] fp16
@@ -155,7 +159,7 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
   if (!xh_in)
     e = ancha::launch_norm_half(x, static_cast<int>(rows), static_cast<int>(dim), nullptr,
                                 nullptr, xh, stream);
-  if (e != hipSuccess) return -static_cast<int>(e);
+  if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_block_forward");
   int rc = gemm(xh, true, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
                 split ? split : 1, inner, nullptr, packed, true, false, stream, kLog2eHost);
   if (rc) return rc;
@@ -184,7 +188,7 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
     ap.tstep = 1;
   }
   e = ancha::launch_attention(ap, true, stream);
-  if (e != hipSuccess) return -static_cast<int>(e);
+  if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_block_forward");
   // x1 = x + attended . W_out
   rc = gemm(attended, true, rows, inner, b->out_w, dim, nullptr, false, nullptr, 0, 1, 0, x, x1,
             false, false, stream);
@@ -192,7 +196,7 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
   // hidden = GELU(fp16(unit_norm(x1)) . W1' + b1), stored fp16.
   e = ancha::launch_norm_half(x1, static_cast<int>(rows), static_cast<int>(dim), nullptr, nullptr,
                               xh, stream);
-  if (e != hipSuccess) return -static_cast<int>(e);
+  if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_block_forward");
   rc = gemm(xh, true, rows, dim, b->ff_in_w, b->hidden, b->ff_in_b, true, nullptr, 0, 1, 0,
             nullptr, hidden, true, false, stream);
   if (rc) return rc;
@@ -204,7 +208,7 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
     // out = unit_norm(out) * scale in place, and the next block's fp16 operand in one pass.
     e = ancha::launch_norm_half(out, static_cast<int>(rows), static_cast<int>(dim), b->out_scale,
                                 out, xh, stream);
-    if (e != hipSuccess) return -static_cast<int>(e);
+    if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_block_forward");
   } else if (b->out_scale) {
     rc = ancha_hip_unit_norm(out, rows, dim, dim, b->out_scale, out, stream);
   }
@@ -223,11 +227,15 @@ int axis_pair_forward_chained(const ancha_hip_block* time, const ancha_hip_block
                               const float* time_rope, const float* band_rope, void* workspace,
                               size_t workspace_bytes, float* out, hipStream_t stream, bool xh_in,
                               bool xh_out) {
-  if (!time || !band || time->dim != band->dim) return ANCHA_HIP_INVALID;
+  static const std::string kWhere = "ancha_hip_axis_pair_forward: ";
+  if (!time || !band || time->dim != band->dim)
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null blocks or blocks of different dim");
   const size_t rows = batch * bands * frames;
   if (rows == 0) return ANCHA_HIP_OK;
-  if (!x || !out || !time_rope || !band_rope || !workspace) return ANCHA_HIP_INVALID;
-  if (workspace_bytes < ancha_hip_axis_pair_workspace(time, band, rows)) return ANCHA_HIP_INVALID;
+  if (!x || !out || !time_rope || !band_rope || !workspace)
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null buffer");
+  if (workspace_bytes < ancha_hip_axis_pair_workspace(time, band, rows))
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "workspace too small");
   const bool inner = block_chainable(time, band);
   // Time pass: groups = batch * bands, sequence = frames, x -> out.
   int rc = block_forward(time, x, batch * bands, frames, 0, time_rope, workspace, workspace_bytes,
@@ -249,22 +257,25 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
                            const float* ff_gamma, const float* ff_in, const float* ff_in_bias,
                            const float* ff_out, const float* ff_out_bias,
                            const float* output_gamma, ancha_hip_block** block) {
-  if (!block) return ANCHA_HIP_INVALID;
+  static const std::string kWhere = "ancha_hip_block_create: ";
+  if (const int s = ancha::sticky()) return s;
+  if (!block) return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null block out-pointer");
   *block = nullptr;
   if (!attn_gamma || !to_qkv || !to_gates || !to_gates_bias || !to_out || !ff_gamma || !ff_in ||
       !ff_in_bias || !ff_out || !ff_out_bias || dim == 0 || heads == 0 || hidden == 0)
-    return ANCHA_HIP_INVALID;
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null weight or zero size");
   const size_t inner = heads * kHeadDim;
   const size_t columns = round_up(3 * inner + heads, 128);
   // forward_kernels' shape gate (roformer.rs:471-475).
   if (!ancha_hip_linear_supported(dim, columns) || !ancha_hip_linear_supported(inner, dim) ||
       !ancha_hip_linear_supported(dim, hidden) || !ancha_hip_linear_supported(hidden, dim))
-    return ANCHA_HIP_UNSUPPORTED;
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "a projection fails linear_supported");
 
-  if (!ancha_hip_available()) return ANCHA_HIP_UNSUPPORTED;
+  if (!ancha_hip_available())
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "not a gfx950 device");
   if (dim * 4 * 128 >= (size_t(1) << 31) || hidden * 4 * 128 >= (size_t(1) << 31) ||
       columns * 4 * 128 >= (size_t(1) << 31))
-    return ANCHA_HIP_UNSUPPORTED;
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "widths exceed the kernels' ranges");
 
   const std::vector<float> norm = source_scale(attn_gamma, dim);
   const std::vector<float> ffs = source_scale(ff_gamma, dim);
@@ -282,7 +293,7 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
   if (output_gamma) os = source_scale(output_gamma, dim);
 
   auto* b = new (std::nothrow) ancha_hip_block{};
-  if (!b) return ANCHA_HIP_INVALID;
+  if (!b) return ancha::fail(ANCHA_HIP_INVALID, kWhere + "out of host memory");
   b->dim = dim;
   b->heads = heads;
   b->hidden = hidden;
@@ -315,6 +326,7 @@ size_t ancha_hip_block_workspace(const ancha_hip_block* b, size_t rows) {
 int ancha_hip_block_forward(const ancha_hip_block* b, const float* x, size_t groups,
                             size_t tokens, const float* rope, void* workspace,
                             size_t workspace_bytes, float* out, hipStream_t stream) {
+  if (const int s = ancha::sticky()) return s;
   return block_forward(b, x, groups, tokens, 0, rope, workspace, workspace_bytes, out, stream);
 }
 
@@ -329,6 +341,7 @@ int ancha_hip_axis_pair_forward(const ancha_hip_block* time, const ancha_hip_blo
                                 const float* x, size_t batch, size_t bands, size_t frames,
                                 const float* time_rope, const float* band_rope, void* workspace,
                                 size_t workspace_bytes, float* out, hipStream_t stream) {
+  if (const int s = ancha::sticky()) return s;
   return ancha::axis_pair_forward_chained(time, band, x, batch, bands, frames, time_rope,
                                           band_rope, workspace, workspace_bytes, out, stream,
                                           false, false);

@@ -11,22 +11,27 @@
 
 #include "../../include/ancha_hip.h"
 #include "kernels.hpp"
+#include "status.hpp"
 
 namespace {
 
 std::atomic<int> g_sticky{0};
 thread_local std::string g_last;
 
+}  // namespace
+
+namespace ancha {
+
 int fail(int code, const std::string& msg) {
   g_last = msg;
   return code;
 }
 
-int hip_fail(hipError_t e, const char* where) {
+int hip_fail(hipError_t e, const std::string& where) {
   const int code = -static_cast<int>(e);
   int expected = 0;
   g_sticky.compare_exchange_strong(expected, code);
-  g_last = std::string(where) + ": " + hipGetErrorString(e);
+  g_last = where + ": " + hipGetErrorString(e);
   return code;
 }
 
@@ -35,6 +40,14 @@ int sticky() {
   if (s) g_last = "an earlier HIP call failed (sticky device failure " + std::to_string(s) + ")";
   return s;
 }
+
+}  // namespace ancha
+
+namespace {
+
+using ancha::fail;
+using ancha::hip_fail;
+using ancha::sticky;
 
 // Per-device cache: 1 = gfx950, 0 = other, -1 = unknown.
 constexpr int kMaxDevices = 64;
@@ -66,8 +79,8 @@ constexpr size_t kIntMax = 0x7fffffff;
 int run_attention(ancha::AttnParams& p, size_t groups, size_t tokens, size_t heads,
                   hipStream_t stream, const char* name) {
   if (groups == 0 || tokens == 0 || heads == 0) return ANCHA_HIP_OK;
-  const size_t qblocks = (tokens + 127) / 128;
-  if (tokens > kIntMax || groups * heads > kIntMax || groups * heads * qblocks > kIntMax)
+  if (tokens > kIntMax || groups > kIntMax || heads > kIntMax ||
+      !ancha::attention_grid_fits(groups, tokens, heads))
     return fail(ANCHA_HIP_UNSUPPORTED, std::string(name) + ": problem count exceeds the grid");
   // The kernels address one (group, head) sequence through 32-bit buffer ranges of
   // (tokens - 1) rows of stride plus one row, in bytes.

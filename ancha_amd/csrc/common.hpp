@@ -39,6 +39,17 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// True for +-inf and NaN. A bit test: the library is compiled with -fno-honor-nans, under which
+// isfinite() may fold to true.
+__device__ __forceinline__ bool non_finite(float x) {
+  return (__builtin_bit_cast(unsigned, x) & 0x7f800000u) == 0x7f800000u;
+}
+
+// ORs `bit` into the device check word (a vector-memory atomic).
+__device__ __forceinline__ void raise_flag(unsigned* flags, unsigned bit) {
+  __hip_atomic_fetch_or(flags, bit, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // Maximum over the four lanes {l, l^16, l^32, l^48} that share a column of an MFMA tile.
 __device__ __forceinline__ float max_over_rows(float x) {
   x = fmaxf(x, __shfl_xor(x, 16));

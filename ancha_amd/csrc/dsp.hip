@@ -11,6 +11,7 @@
 // Layouts: audio / chunks [2][samples]; the model spectrum [frames][bins][channel][re, im]
 // (runtime.rs:161-172, the band-split input); masks [rows = 2*bins][re, im][frames] per stem
 // (network.rs Roformer::forward output); frames scratch [frames][2][n_fft].
+#include "common.hpp"
 #include "kernels.hpp"
 
 namespace ancha {
@@ -133,7 +134,8 @@ __global__ __launch_bounds__(kFftThreads) void istft_frames_kernel(const float* 
 // sums [2][total], weights [total] (updated only when `count_weight`).
 __global__ void ola_accumulate_kernel(const float* frames_buf, int frames, int hop,
                                       long length, long start, long total, int first, int last,
-                                      int count_weight, float* sums, float* weights) {
+                                      int count_weight, float* sums, float* weights,
+                                      unsigned* flags) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= length) return;
   const long pos = start + i;
@@ -154,14 +156,20 @@ __global__ void ola_accumulate_kernel(const float* frames_buf, int frames, int h
   float wt = 1.0f;
   if (!first && i < fade) wt = (float)(i + 1) / (float)fade;
   if (!last && i >= length - fade) wt = (float)(length - i) / (float)fade;
-  sums[pos] += wt * (a0 / den);
-  sums[total + pos] += wt * (a1 / den);
+  const float y0 = a0 / den, y1 = a1 / den;
+  if (flags) {
+    if (!(den > 1e-11f)) raise_flag(flags, kFlagIstftUncovered);
+    if (non_finite(y0) || non_finite(y1)) raise_flag(flags, kFlagChunk);
+  }
+  sums[pos] += wt * y0;
+  sums[total + pos] += wt * y1;
   if (count_weight) weights[pos] += wt;
 }
 
 // Chunk extraction of runtime.rs:118-136: reflect-bordered samples of the clip.
 __global__ void chunk_gather_kernel(const float* audio, long n, long start, long border,
-                                    long remaining, long samples, float* chunk) {
+                                    long remaining, long samples, float* chunk,
+                                    unsigned* flags) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= samples) return;
   float v0 = 0.0f, v1 = 0.0f;
@@ -171,6 +179,7 @@ __global__ void chunk_gather_kernel(const float* audio, long n, long start, long
     v0 = audio[src];
     v1 = audio[n + src];
   }
+  if (flags && (non_finite(v0) || non_finite(v1))) raise_flag(flags, kFlagInput);
   chunk[i] = v0;
   chunk[samples + i] = v1;
 }
@@ -178,10 +187,12 @@ __global__ void chunk_gather_kernel(const float* audio, long n, long start, long
 // Accumulator::finish + border crop (chunk.rs:75-88, runtime.rs:215-223); optionally the
 // residual input - stem (runtime.rs:403-420).
 __global__ void finish_kernel(const float* sums, const float* weights, long total, long border,
-                              long n, const float* audio, float* out, float* residual) {
+                              long n, const float* audio, float* out, float* residual,
+                              unsigned* flags) {
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= n) return;
   const float w = weights[border + i];
+  if (flags && !(w > 0.0f)) raise_flag(flags, kFlagOlaUncovered);
   for (int c = 0; c < 2; c++) {
     const float y = sums[c * total + border + i] / w;
     out[c * n + i] = y;
@@ -215,24 +226,27 @@ hipError_t launch_istft_frames(const float* spectrum, const float* masks, int fr
 
 hipError_t launch_ola_accumulate(const float* frames_buf, int frames, int hop, long length,
                                  long start, long total, bool first, bool last, bool count_weight,
-                                 float* sums, float* weights, hipStream_t stream) {
+                                 float* sums, float* weights, unsigned* flags,
+                                 hipStream_t stream) {
   hipLaunchKernelGGL(ola_accumulate_kernel, dim3(blocks_for(length, 256)), dim3(256), 0, stream,
                      frames_buf, frames, hop, length, start, total, (int)first, (int)last,
-                     (int)count_weight, sums, weights);
+                     (int)count_weight, sums, weights, flags);
   return hipGetLastError();
 }
 
 hipError_t launch_chunk_gather(const float* audio, long n, long start, long border,
-                               long remaining, long samples, float* chunk, hipStream_t stream) {
+                               long remaining, long samples, float* chunk, unsigned* flags,
+                               hipStream_t stream) {
   hipLaunchKernelGGL(chunk_gather_kernel, dim3(blocks_for(samples, 256)), dim3(256), 0, stream,
-                     audio, n, start, border, remaining, samples, chunk);
+                     audio, n, start, border, remaining, samples, chunk, flags);
   return hipGetLastError();
 }
 
 hipError_t launch_finish(const float* sums, const float* weights, long total, long border, long n,
-                         const float* audio, float* out, float* residual, hipStream_t stream) {
+                         const float* audio, float* out, float* residual, unsigned* flags,
+                         hipStream_t stream) {
   hipLaunchKernelGGL(finish_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, sums, weights,
-                     total, border, n, audio, out, residual);
+                     total, border, n, audio, out, residual, flags);
   return hipGetLastError();
 }
 

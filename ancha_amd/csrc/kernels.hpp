@@ -34,6 +34,10 @@ struct AttnParams {
 // `aligned`: every float4 access is 16-byte aligned (base pointers and row strides).
 hipError_t launch_attention(const AttnParams& p, bool aligned, hipStream_t stream);
 
+// Whether the launch launch_attention picks for this shape fits HIP's grid limits (workgroup
+// count below 2^31 and total thread count below 2^32).
+bool attention_grid_fits(size_t groups, size_t tokens, size_t heads);
+
 // out = epilogue(x . w): x [n, k] (row stride ldx), w [k, m] row-major (the reference's
 // [in, out] Linear layout), out [n, m] contiguous. Epilogue, in order: optional input row norm
 // (the product of row r scaled by 1 / max(||x_r||, 1e-12)), bias [m], erf-GELU, interleaved
@@ -125,6 +129,16 @@ int axis_pair_forward_chained(const ancha_hip_block* time, const ancha_hip_block
                               size_t workspace_bytes, float* out, hipStream_t stream, bool xh_in,
                               bool xh_out);
 
+// Check flags of one separation: the kernels below OR these bits into a device word (`flags`,
+// or null for no checks) where they meet what the reference runtime rejects.
+enum : unsigned {
+  kFlagInput = 1u,          // non-finite STFT input (dsp.rs:57-60)
+  kFlagMasks = 2u,          // non-finite model output (runtime.rs:173-176)
+  kFlagIstftUncovered = 4u, // iSTFT window sum <= 1e-11 at an output sample (dsp.rs:126)
+  kFlagChunk = 8u,          // non-finite iSTFT / chunk output (dsp.rs:128-131, chunk.rs:57-60)
+  kFlagOlaUncovered = 16u,  // overlap-add weight <= 0 at an output sample (chunk.rs:76-79)
+};
+
 // Separation runtime (dsp.hip), n_fft = 2048. chunk / audio [2][samples]; spectrum
 // [frames][1025][channel][re, im]; masks [2050][re, im][frames] (one stem); frames_buf
 // [frames][2][2048]; sums [2][total], weights [total].
@@ -134,12 +148,26 @@ hipError_t launch_istft_frames(const float* spectrum, const float* masks, int fr
                                float* frames_buf, hipStream_t stream);
 hipError_t launch_ola_accumulate(const float* frames_buf, int frames, int hop, long length,
                                  long start, long total, bool first, bool last, bool count_weight,
-                                 float* sums, float* weights, hipStream_t stream);
+                                 float* sums, float* weights, unsigned* flags, hipStream_t stream);
 hipError_t launch_chunk_gather(const float* audio, long n, long start, long border,
-                               long remaining, long samples, float* chunk, hipStream_t stream);
+                               long remaining, long samples, float* chunk, unsigned* flags,
+                               hipStream_t stream);
 hipError_t launch_finish(const float* sums, const float* weights, long total, long border, long n,
-                         const float* audio, float* out, float* residual, hipStream_t stream);
+                         const float* audio, float* out, float* residual, unsigned* flags,
+                         hipStream_t stream);
 hipError_t launch_zero(float* p, long n, hipStream_t stream);
+
+// Packed rotary tables of AxisRope::new (roformer.rs:282-302) for `sets` frequency sets, built
+// on the device: freqs [sets][32] -> out [sets][4][tokens][64] (query cos and signed sin times
+// 1/8, key cos and signed sin; angle = f32(t) * f).
+hipError_t launch_axis_rope(const float* freqs, int sets, int tokens, float* out,
+                            hipStream_t stream);
+// Tile tables of the mask heads' grouped product (Gemm16Params::group_*) for `row_tiles` row
+// tiles per band: band b owns tiles [first[b], first[b+1]) with first[b] = row_tiles *
+// col0[b] / 128; of_tile[t] = the band of tile t (total = row_tiles * col0[bands] / 128 tiles;
+// first has bands + 1 entries).
+hipError_t launch_group_tiles(const long* col0, int bands, int row_tiles, long total,
+                              int* of_tile, int* first, hipStream_t stream);
 
 // Band split (mel.hip): spectrum [frames][cols]; band b = FFT bins bins[offsets[b] ..
 // offsets[b+1]), feature columns 4*bin .. 4*bin+3; weight: per band [width][dim] fp32 (folded
@@ -170,6 +198,7 @@ struct GluParams {
   const int* cover_band;
   const int* cover_local;
   float* masks;
+  unsigned* flags;  // kFlagMasks on a non-finite mask value (or null)
   int outputs, frames;
 };
 hipError_t launch_glu_gather(const GluParams& p, hipStream_t stream);

@@ -12,6 +12,7 @@
 //    number, written in the reference's [row = 2*bin + channel][re, im][frame] layout.
 //    Each output gathers its 1..k covering bands from a host-built table (no atomics, the
 //    summation order is the band order).
+#include "common.hpp"
 #include "kernels.hpp"
 
 namespace ancha {
@@ -118,7 +119,9 @@ __global__ void glu_gather_kernel(GluParams p) {
     const float value = row[col], gate = row[p.band_width[b] + col];
     sum += value * (1.0f / (1.0f + expf(-gate)));
   }
-  p.masks[(long)o * p.frames + t] = sum / (float)(e1 - e0);
+  const float mask = sum / (float)(e1 - e0);
+  if (p.flags && non_finite(mask)) raise_flag(p.flags, kFlagMasks);
+  p.masks[(long)o * p.frames + t] = mask;
 }
 
 }  // namespace

@@ -12,6 +12,7 @@
 // Weights come from a callback that serves the reference checkpoint's tensors by name.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <new>
@@ -20,6 +21,7 @@
 
 #include "../../include/ancha_hip.h"
 #include "kernels.hpp"
+#include "status.hpp"
 
 namespace {
 
@@ -35,29 +37,17 @@ int upload(const std::vector<T>& host, T** dev) {
   hipError_t e = hipMalloc(reinterpret_cast<void**>(dev), host.size() * sizeof(T));
   if (e == hipSuccess)
     e = hipMemcpy(*dev, host.data(), host.size() * sizeof(T), hipMemcpyHostToDevice);
-  return e == hipSuccess ? 0 : -static_cast<int>(e);
+  return ancha::hip_status(e, "ancha_hip_roformer_create: weight upload");
 }
 
-// AxisRope::new (roformer.rs:282-302): [4][tokens][64] = query cos, query signed sin (both
-// times 1/sqrt(64)), key cos, key signed sin; angle = f32(t) * f.
-std::vector<float> axis_rope(const std::vector<float>& freqs, size_t tokens) {
-  const size_t nf = freqs.size(), width = 2 * nf;
-  const float scale = 1.0f / std::sqrt(static_cast<float>(width));
-  std::vector<float> out(4 * tokens * width);
-  size_t p = 0;
-  for (int table = 0; table < 2; table++) {
-    const float s_ = table == 0 ? scale : 1.0f;
-    for (int sine = 0; sine < 2; sine++)
-      for (size_t t = 0; t < tokens; t++)
-        for (size_t i = 0; i < nf; i++) {
-          const float angle = static_cast<float>(t) * freqs[i];
-          const float s = std::sin(angle), c = std::cos(angle);
-          out[p++] = sine ? -s * s_ : c * s_;
-          out[p++] = sine ? s * s_ : c * s_;
-        }
-  }
-  return out;
+template <typename T>
+int alloc(size_t count, T** dev) {
+  *dev = nullptr;
+  return ancha::hip_status(hipMalloc(reinterpret_cast<void**>(dev), count * sizeof(T)),
+                           "ancha_hip_roformer_create: table allocation");
 }
+
+constexpr size_t kRopeFloats = 4 * kHeadDim;  // per token of one packed rotary table
 
 }  // namespace
 
@@ -83,15 +73,19 @@ struct ancha_hip_roformer {
   long* d_band_base = nullptr;
   int *d_band_stride = nullptr, *d_band_width = nullptr;
   int *d_cover_start = nullptr, *d_cover_band = nullptr, *d_cover_local = nullptr;
-  // Rotary tables [4][tokens][64] per block, for the frame count they were built for.
-  size_t rope_frames = 0;
-  std::vector<float*> time_rope, band_rope;
+  // Rotary frequencies [2 * depth][32] (the time sets, then the frequency sets) and the packed
+  // rotary tables built from them at load time: time [depth][4][frames][64] for the chunk's
+  // frame count, frequency [depth][4][bands][64]. A forward over another frame count builds its
+  // time tables in its workspace instead.
+  size_t frames = 0;
+  float* d_freqs = nullptr;
+  float *time_rope = nullptr, *band_rope = nullptr;
   // The value|gate projections of all bands as one grouped product: per band output width and
-  // first column; per frame count, the band of each tile and each band's first tile.
+  // first column (bands + 1 entries); for the chunk's frame count, the band of each tile and
+  // each band's first tile.
   int* d_group_cols = nullptr;
   long* d_group_col0 = nullptr;
   int *d_group_of_tile = nullptr, *d_group_first = nullptr;
-  int group_tiles = 0;
 };
 
 namespace {
@@ -105,7 +99,9 @@ void free_all(ancha_hip_roformer* m) {
                   static_cast<void*>(m->d_band_width), static_cast<void*>(m->d_cover_start),
                   static_cast<void*>(m->d_cover_band), static_cast<void*>(m->d_cover_local),
                   static_cast<void*>(m->d_group_cols), static_cast<void*>(m->d_group_col0),
-                  static_cast<void*>(m->d_group_of_tile), static_cast<void*>(m->d_group_first)})
+                  static_cast<void*>(m->d_group_of_tile), static_cast<void*>(m->d_group_first),
+                  static_cast<void*>(m->d_freqs), static_cast<void*>(m->time_rope),
+                  static_cast<void*>(m->band_rope)})
     if (p) (void)hipFree(p);
   for (auto* b : m->blocks) ancha_hip_block_destroy(b);
   for (auto& h : m->mask_heads) {
@@ -114,8 +110,6 @@ void free_all(ancha_hip_roformer* m) {
     if (h.ow) (void)hipFree(h.ow);
     if (h.ob) (void)hipFree(h.ob);
   }
-  for (auto* p : m->time_rope) (void)hipFree(p);
-  for (auto* p : m->band_rope) (void)hipFree(p);
   delete m;
 }
 
@@ -143,55 +137,34 @@ int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, siz
   p.w_bstride = w_bstride;
   p.bias_bstride = bias_bstride;
   p.out_bstride = out_bstride;
-  const hipError_t e = ancha::launch_gemm16(p, stream);
-  return e == hipSuccess ? 0 : -static_cast<int>(e);
+  return ancha::hip_status(ancha::launch_gemm16(p, stream), "mask head GEMM");
 }
 
-// Rotary tables for `frames` time steps (built on first use of a frame count).
-int ensure_rope(ancha_hip_roformer* m, size_t frames) {
-  if (m->rope_frames == frames) return 0;
-  for (auto* p : m->time_rope) (void)hipFree(p);
-  for (auto* p : m->band_rope) (void)hipFree(p);
-  for (int* p : {m->d_group_of_tile, m->d_group_first})
-    if (p) (void)hipFree(p);
-  m->d_group_of_tile = m->d_group_first = nullptr;
-  m->time_rope.assign(m->depth, nullptr);
-  m->band_rope.assign(m->depth, nullptr);
-  m->rope_frames = 0;
-  for (size_t i = 0; i < m->depth; i++) {
-    int rc = upload(axis_rope(m->freqs[2 * i], frames), &m->time_rope[i]);
-    if (!rc) rc = upload(axis_rope(m->freqs[2 * i + 1], m->bands), &m->band_rope[i]);
-    if (rc) return rc;
-  }
-  // Tiles of the grouped value|gate product: band b has row tiles x (mpad[b] / 128) of them.
-  const size_t row_tiles = (frames + 127) / 128;
-  std::vector<int> of_tile, first(m->bands);
-  for (size_t b = 0; b < m->bands; b++) {
-    first[b] = static_cast<int>(of_tile.size());
-    of_tile.insert(of_tile.end(), row_tiles * (m->mpad[b] / 128), static_cast<int>(b));
-  }
-  if (of_tile.size() > 0x7fffffff) return ANCHA_HIP_UNSUPPORTED;
-  int rc = upload(of_tile, &m->d_group_of_tile);
-  if (!rc) rc = upload(first, &m->d_group_first);
-  if (rc) return rc;
-  m->group_tiles = static_cast<int>(of_tile.size());
-  m->rope_frames = frames;
-  return 0;
+// Tiles of the grouped value|gate product over `frames` frames: band b has row tiles x
+// (mpad[b] / 128) of them.
+size_t group_tiles(const ancha_hip_roformer* m, size_t frames) {
+  return (frames + 127) / 128 * (m->colprefix.back() / 128);
 }
 
 // Workspace regions of a forward over `frames` frames.
 struct Layout {
-  size_t x, inner, h1, h2, glu, xh, total;
+  size_t tables, x, inner, h1, h2, glu, xh, total;
 };
 // nch chunks share the axis loop (x [nch][bands][frames][dim]); the mask heads run one chunk
-// at a time in the same head buffers.
+// at a time in the same head buffers. A frame count other than the chunk's first gets its
+// rotary and tile tables (region `tables`, rebuilt on the device by every forward).
 Layout forward_layout(const ancha_hip_roformer* m, size_t frames, size_t nch = 1) {
   Layout l{};
   const size_t rows = m->bands * frames;
-  l.x = 0;
+  size_t tables = 0;
+  if (frames != m->frames)
+    tables = round_up(m->depth * frames * kRopeFloats * 4, 256) +
+             round_up((group_tiles(m, frames) + m->bands + 1) * 4, 256);
+  l.tables = 0;
+  l.x = tables;
   const size_t block_ws =
       ancha_hip_axis_pair_workspace(m->blocks[0], m->blocks[1], nch * rows);
-  l.inner = round_up(nch * rows * m->dim * 4, 256);
+  l.inner = l.x + round_up(nch * rows * m->dim * 4, 256);
   l.h1 = l.inner;
   l.h2 = l.h1 + round_up(rows * m->mask_hidden * 2, 256);
   l.glu = l.h2 + round_up(rows * m->mask_hidden * 2, 256);
@@ -203,15 +176,45 @@ Layout forward_layout(const ancha_hip_roformer* m, size_t frames, size_t nch = 1
   return l;
 }
 
-// Forward of nch chunks' spectra (1 or 2) into their masks.
+bool cancel_requested(const volatile int* cancelled) { return cancelled && *cancelled != 0; }
+
+int cancelled_rc() { return ancha::fail(ANCHA_HIP_CANCELLED, "task cancelled"); }
+
+// Forward of nch chunks' spectra (1 or 2) into their masks. `flags` (or null) collects the
+// non-finite mask check of the separation runtime. Returns ANCHA_HIP_CANCELLED when
+// *cancelled is set at a layer pair or a mask head (network.rs:334,367); what was enqueued
+// before still runs.
 int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch, size_t frames,
-                 void* workspace, float* const* masks_of, hipStream_t stream) {
+                 void* workspace, float* const* masks_of, const volatile int* cancelled,
+                 unsigned* flags, hipStream_t stream) {
+  static const char* kWhere = "ancha_hip_roformer_forward";
   unsigned char* ws = static_cast<unsigned char*>(workspace);
   const Layout l = forward_layout(m, frames, nch);
   float* x = reinterpret_cast<float*>(ws + l.x);
   const size_t rows = m->bands * frames;
-  int rc = ensure_rope(m, frames);
-  if (rc) return rc;
+  const size_t table_floats = frames * kRopeFloats;
+  // Rotary and tile tables: the model's own for the chunk's frame count, else built here.
+  const float* time_rope = m->time_rope;
+  const int* of_tile = m->d_group_of_tile;
+  const int* first_tile = m->d_group_first;
+  if (frames != m->frames) {
+    float* rope = reinterpret_cast<float*>(ws + l.tables);
+    int* tiles = reinterpret_cast<int*>(ws + l.tables +
+                                        round_up(m->depth * table_floats * 4, 256));
+    const size_t ntiles = group_tiles(m, frames);
+    if (frames * kRopeFloats * m->depth > 0x7fffffff || ntiles > 0x7fffffff)
+      return ancha::fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_roformer_forward: too many frames");
+    hipError_t e = ancha::launch_axis_rope(m->d_freqs, static_cast<int>(m->depth),
+                                           static_cast<int>(frames), rope, stream);
+    if (e == hipSuccess)
+      e = ancha::launch_group_tiles(m->d_group_col0, static_cast<int>(m->bands),
+                                    static_cast<int>((frames + 127) / 128),
+                                    static_cast<long>(ntiles), tiles, tiles + ntiles, stream);
+    if (e != hipSuccess) return ancha::hip_fail(e, kWhere);
+    time_rope = rope;
+    of_tile = tiles;
+    first_tile = tiles + ntiles;
+  }
   ancha::BandSplitParams bp{};
   bp.offsets = m->d_offsets;
   bp.bins = m->d_bins;
@@ -224,29 +227,29 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
   bp.cols = static_cast<int>(4 * m->fft_bins);
   bp.dim = static_cast<int>(m->dim);
   bp.max_width = static_cast<int>(m->max_width);
-  hipError_t e = hipSuccess;
-  for (size_t c = 0; c < nch && e == hipSuccess; c++) {
+  for (size_t c = 0; c < nch; c++) {
     bp.spectrum = spectra[c];
     bp.x = x + c * rows * m->dim;
-    e = ancha::launch_band_split(bp, stream);
+    if (const int rc = ancha::hip_status(ancha::launch_band_split(bp, stream), kWhere)) return rc;
   }
-  if (e != hipSuccess) return -static_cast<int>(e);
   // Axis loop (network.rs:333-339): x [nch][bands][frames][dim] is the time layout with batch
   // nch.
   const size_t block_bytes = l.total - l.inner;
   // Each block's output norm also writes the next block's fp16 operand where the blocks allow.
   bool xh_in = false;
   for (size_t i = 0; i < m->depth; i++) {
+    if (cancel_requested(cancelled)) return cancelled_rc();
     const bool xh_out =
         i + 1 < m->depth && ancha::block_chainable(m->blocks[2 * i + 1], m->blocks[2 * i + 2]);
-    rc = ancha::axis_pair_forward_chained(m->blocks[2 * i], m->blocks[2 * i + 1], x, nch, m->bands,
-                                          frames, m->time_rope[i], m->band_rope[i], ws + l.inner,
-                                          block_bytes, x, stream, xh_in, xh_out);
+    const int rc = ancha::axis_pair_forward_chained(
+        m->blocks[2 * i], m->blocks[2 * i + 1], x, nch, m->bands, frames,
+        time_rope + i * table_floats, m->band_rope + i * m->bands * kRopeFloats, ws + l.inner,
+        block_bytes, x, stream, xh_in, xh_out);
     if (rc) return rc;
     xh_in = xh_out;
   }
   if (m->final_scale) {
-    rc = ancha_hip_unit_norm(x, nch * rows, m->dim, m->dim, m->final_scale, x, stream);
+    const int rc = ancha_hip_unit_norm(x, nch * rows, m->dim, m->dim, m->final_scale, x, stream);
     if (rc) return rc;
   }
   _Float16* h[2] = {reinterpret_cast<_Float16*>(ws + l.h1), reinterpret_cast<_Float16*>(ws + l.h2)};
@@ -254,13 +257,15 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
   _Float16* xh = reinterpret_cast<_Float16*>(ws + l.xh);
   const bool cast = m->dim % 8 == 0;
   if (cast) {
-    e = ancha::launch_cast_half(x, static_cast<long>(nch * rows * m->dim), xh, stream);
-    if (e != hipSuccess) return -static_cast<int>(e);
+    const int rc = ancha::hip_status(
+        ancha::launch_cast_half(x, static_cast<long>(nch * rows * m->dim), xh, stream), kWhere);
+    if (rc) return rc;
   }
   float* glu = reinterpret_cast<float*>(ws + l.glu);
   const size_t mh = m->mask_hidden;
   for (size_t c = 0; c < nch; c++)
   for (size_t s = 0; s < m->stems; s++) {
+    if (cancel_requested(cancelled)) return cancelled_rc();
     const ancha_hip_roformer::Head& head = m->mask_heads[s];
     // Hidden layers (network.rs:377-379): h = tanh(W h + b) per band, fp16 between layers.
     const void* in = cast ? static_cast<const void*>(xh + c * rows * m->dim)
@@ -269,9 +274,10 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
     size_t in_dim = m->dim;
     for (size_t layer = 0; layer < m->mask_layers; layer++) {
       _Float16* out = h[layer & 1];
-      rc = gemm(in, in_half, frames, in_dim, head.hw[layer], mh, head.hb[layer], true, out, true,
-                m->bands, static_cast<long>(frames * in_dim), static_cast<long>(mh * in_dim),
-                static_cast<long>(mh), static_cast<long>(frames * mh), stream);
+      const int rc = gemm(in, in_half, frames, in_dim, head.hw[layer], mh, head.hb[layer], true,
+                          out, true, m->bands, static_cast<long>(frames * in_dim),
+                          static_cast<long>(mh * in_dim), static_cast<long>(mh),
+                          static_cast<long>(frames * mh), stream);
       if (rc) return rc;
       in = out;
       in_half = true;
@@ -279,29 +285,26 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
     }
     // Output projection, value and gate halves side by side: one grouped product over the
     // bands (band b: [frames, mh] x [mh, mpad[b]] into glu + colprefix[b] * frames).
-    {
-      ancha::Gemm16Params gp16{};
-      gp16.x = in;
-      gp16.wt = head.ow;
-      gp16.bias = head.ob;
-      gp16.out = glu;
-      gp16.ldx = static_cast<long>(mh);
-      gp16.n = static_cast<int>(frames);
-      gp16.k = static_cast<int>(mh);
-      gp16.m = 128;
-      gp16.tokens = 1;
-      gp16.token_div = 1;
-      gp16.x_half = 1;
-      gp16.batch = static_cast<int>(m->bands);
-      gp16.x_bstride = static_cast<long>(frames * mh);
-      gp16.group_of_tile = m->d_group_of_tile;
-      gp16.group_first_tile = m->d_group_first;
-      gp16.group_cols = m->d_group_cols;
-      gp16.group_col0 = m->d_group_col0;
-      gp16.group_tiles = m->group_tiles;
-      e = ancha::launch_gemm16(gp16, stream);
-      if (e != hipSuccess) return -static_cast<int>(e);
-    }
+    ancha::Gemm16Params gp16{};
+    gp16.x = in;
+    gp16.wt = head.ow;
+    gp16.bias = head.ob;
+    gp16.out = glu;
+    gp16.ldx = static_cast<long>(mh);
+    gp16.n = static_cast<int>(frames);
+    gp16.k = static_cast<int>(mh);
+    gp16.m = 128;
+    gp16.tokens = 1;
+    gp16.token_div = 1;
+    gp16.x_half = 1;
+    gp16.batch = static_cast<int>(m->bands);
+    gp16.x_bstride = static_cast<long>(frames * mh);
+    gp16.group_of_tile = of_tile;
+    gp16.group_first_tile = first_tile;
+    gp16.group_cols = m->d_group_cols;
+    gp16.group_col0 = m->d_group_col0;
+    gp16.group_tiles = static_cast<int>(group_tiles(m, frames));
+    if (const int rc = ancha::hip_status(ancha::launch_gemm16(gp16, stream), kWhere)) return rc;
     ancha::GluParams gp{};
     gp.glu = glu;
     gp.band_base = m->d_band_base;
@@ -311,10 +314,10 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
     gp.cover_band = m->d_cover_band;
     gp.cover_local = m->d_cover_local;
     gp.masks = masks_of[c] + s * 4 * m->fft_bins * frames;
+    gp.flags = flags;
     gp.outputs = static_cast<int>(4 * m->fft_bins);
     gp.frames = static_cast<int>(frames);
-    e = ancha::launch_glu_gather(gp, stream);
-    if (e != hipSuccess) return -static_cast<int>(e);
+    if (const int rc = ancha::hip_status(ancha::launch_glu_gather(gp, stream), kWhere)) return rc;
   }
   return 0;
 }
@@ -336,7 +339,7 @@ Plan plan_for(const ancha_hip_roformer* m, size_t samples) {
 }
 
 struct SepLayout {
-  size_t chunk, spectrum, masks, frames_buf, sums, weights, model, total;
+  size_t flags, chunk, spectrum, masks, frames_buf, sums, weights, model, total;
 };
 SepLayout separate_layout(const ancha_hip_roformer* m, size_t samples) {
   const Plan p = plan_for(m, samples);
@@ -347,6 +350,7 @@ SepLayout separate_layout(const ancha_hip_roformer* m, size_t samples) {
     o += round_up(bytes, 256);
     return at;
   };
+  l.flags = take(4);
   // Two chunks at a time go through the model together.
   l.chunk = take(2 * 2 * m->chunk * 4);
   l.spectrum = take(2 * p.frames * 4 * m->fft_bins * 4);
@@ -367,36 +371,44 @@ extern "C" {
 
 int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tensor_fn get,
                               void* ctx, ancha_hip_roformer** model) {
-  if (!model) return ANCHA_HIP_INVALID;
+  static const char* kWhere = "ancha_hip_roformer_create: ";
+  auto invalid = [&](const char* why) {
+    return ancha::fail(ANCHA_HIP_INVALID, std::string(kWhere) + why);
+  };
+  if (const int s = ancha::sticky()) return s;
+  if (!model) return invalid("null model out-pointer");
   *model = nullptr;
-  if (!c || !get || !c->band_offsets || !c->band_bins) return ANCHA_HIP_INVALID;
-  if (!ancha_hip_available()) return ANCHA_HIP_UNSUPPORTED;
+  if (!c || !get || !c->band_offsets || !c->band_bins) return invalid("null config or callback");
+  if (!ancha_hip_available())
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, std::string(kWhere) + "not a gfx950 device");
   // Schema checks (config.rs:36-121) plus what the kernels cover.
   if (c->n_fft != kFft || c->head_dim != kHeadDim || c->hop == 0 || c->hop > kFft / 2 ||
       c->dim == 0 || c->depth == 0 || c->heads == 0 || c->ff_mult == 0 || c->mask_depth == 0 ||
       c->mask_expansion == 0 || c->stems == 0 || c->stems > 2 || c->bands < 2 ||
       c->chunk_samples <= kFft / 2 || c->overlap == 0 || c->overlap > c->chunk_samples ||
       (!c->mel && c->mask_depth < 2))
-    return ANCHA_HIP_INVALID;
+    return invalid("config outside the model schema");
   const size_t fft_bins = kFft / 2 + 1;
   std::vector<int> coverage(fft_bins, 0);
   for (size_t b = 0; b < c->bands; b++) {
-    if (c->band_offsets[b + 1] <= c->band_offsets[b]) return ANCHA_HIP_INVALID;
+    if (c->band_offsets[b + 1] <= c->band_offsets[b]) return invalid("empty band");
     for (size_t q = c->band_offsets[b]; q < c->band_offsets[b + 1]; q++) {
-      if (c->band_bins[q] >= fft_bins) return ANCHA_HIP_INVALID;
+      if (c->band_bins[q] >= fft_bins) return invalid("band bin past the FFT bins");
       if (q > c->band_offsets[b] && c->band_bins[q] <= c->band_bins[q - 1])
-        return ANCHA_HIP_INVALID;
+        return invalid("band bins not strictly increasing");
       coverage[c->band_bins[q]]++;
     }
   }
   for (int n : coverage)
-    if (n == 0) return ANCHA_HIP_INVALID;  // "bands leave uncovered FFT bins"
+    if (n == 0) return invalid("bands leave uncovered FFT bins");
   const size_t dim = c->dim, mh = c->dim * c->mask_expansion;
+  // (the band-split kernel covers dim <= 512)
   if (!ancha_hip_linear_supported(dim, mh) || !ancha_hip_linear_supported(mh, mh) || dim > 512)
-    return ANCHA_HIP_UNSUPPORTED;  // (the band-split kernel covers dim <= 512)
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED,
+                       std::string(kWhere) + "dim or mask width outside the kernels");
 
   auto* m = new (std::nothrow) ancha_hip_roformer{};
-  if (!m) return ANCHA_HIP_INVALID;
+  if (!m) return invalid("out of host memory");
   m->mel = c->mel != 0;
   m->zero_dc = c->zero_dc != 0;
   m->dim = dim;
@@ -424,9 +436,13 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
     if (w > m->max_width) m->max_width = w;
   }
   int rc = 0;
-  auto fail = [&](int code) {
+  auto abandon = [&](int code) {
     free_all(m);
     return code;
+  };
+  auto missing = [&](const std::string& name) {
+    return abandon(ancha::fail(ANCHA_HIP_INVALID,
+                               "ancha_hip_roformer_create: missing or mis-shaped tensor " + name));
   };
   auto tensor = [&](const std::string& name, size_t numel) -> const float* {
     return get(ctx, name.c_str(), numel);
@@ -440,7 +456,7 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
       const float* g = tensor(p + ".0.gamma", width);
       const float* wt = tensor(p + ".1.weight", dim * width);
       const float* bs = tensor(p + ".1.bias", dim);
-      if (!g || !wt || !bs) return fail(ANCHA_HIP_INVALID);
+      if (!g || !wt || !bs) return missing(p + ".*");
       const float root = std::sqrt(static_cast<float>(width));
       for (size_t d = 0; d < dim; d++)
         for (size_t col = 0; col < width; col++)
@@ -454,7 +470,7 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
     if (!rc) rc = upload(off, &m->d_offsets);
     if (!rc) rc = upload(bins, &m->d_bins);
     if (!rc) rc = upload(wofs, &m->d_wofs);
-    if (rc) return fail(rc);
+    if (rc) return abandon(rc);
   }
   // Transformer blocks (network.rs:122-137; Transformer::load, roformer.rs:381-409).
   for (size_t i = 0; i < c->depth; i++)
@@ -471,23 +487,23 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
           m->mel ? tensor(p + ".norm.gamma", dim) : nullptr};
       const float* fr = tensor(a + ".rotary_embed.freqs", kHeadDim / 2);
       for (int j = 0; j < 10; j++)
-        if (!t[j]) return fail(ANCHA_HIP_INVALID);
-      if (!fr || (m->mel && !t[10])) return fail(ANCHA_HIP_INVALID);
+        if (!t[j]) return missing(p + ".*");
+      if (!fr || (m->mel && !t[10])) return missing(p + ".*");
       ancha_hip_block* blk = nullptr;
       rc = ancha_hip_block_create(dim, c->heads, hidden, t[0], t[1], t[2], t[3], t[4], t[5], t[6],
                                   t[7], t[8], t[9], t[10], &blk);
-      if (rc) return fail(rc);
+      if (rc) return abandon(rc);
       m->blocks.push_back(blk);
       m->freqs.emplace_back(fr, fr + kHeadDim / 2);
     }
   if (!m->mel) {  // final_norm (network.rs:138-142, :340-342)
     const float* g = tensor("final_norm.gamma", dim);
-    if (!g) return fail(ANCHA_HIP_INVALID);
+    if (!g) return missing("final_norm.gamma");
     std::vector<float> s(dim);
     const float root = std::sqrt(static_cast<float>(dim));
     for (size_t d = 0; d < dim; d++) s[d] = g[d] * root;
     rc = upload(s, &m->final_scale);
-    if (rc) return fail(rc);
+    if (rc) return abandon(rc);
   }
   // Value|gate output width of each band, padded to a multiple of 128, and its first column.
   m->mpad.resize(c->bands);
@@ -498,14 +514,12 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
   }
   {
     std::vector<int> cols(c->bands);
-    std::vector<long> col0(c->bands);
-    for (size_t b = 0; b < c->bands; b++) {
-      cols[b] = static_cast<int>(m->mpad[b]);
-      col0[b] = static_cast<long>(m->colprefix[b]);
-    }
+    std::vector<long> col0(c->bands + 1);
+    for (size_t b = 0; b < c->bands; b++) cols[b] = static_cast<int>(m->mpad[b]);
+    for (size_t b = 0; b <= c->bands; b++) col0[b] = static_cast<long>(m->colprefix[b]);
     rc = upload(cols, &m->d_group_cols);
     if (!rc) rc = upload(col0, &m->d_group_col0);
-    if (rc) return fail(rc);
+    if (rc) return abandon(rc);
   }
   // Mask heads (network.rs:143-177): hidden layers [bands][out][in] fp16, output [m_pad][mh].
   for (size_t s = 0; s < c->stems; s++) {
@@ -523,7 +537,7 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
       for (size_t b = 0; b < c->bands; b++) {
         const float* wt = tensor(key(b, layer) + ".weight", mh * in);
         const float* bs = tensor(key(b, layer) + ".bias", mh);
-        if (!wt || !bs) return fail(ANCHA_HIP_INVALID);
+        if (!wt || !bs) return missing(key(b, layer) + ".*");
         for (size_t e = 0; e < mh * in; e++) w[b * mh * in + e] = static_cast<_Float16>(wt[e]);
         for (size_t o = 0; o < mh; o++) bias[b * mh + o] = bs[o];
       }
@@ -533,7 +547,7 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
       h.hw.push_back(dw);
       if (!rc) rc = upload(bias, &db);
       h.hb.push_back(db);
-      if (rc) return fail(rc);
+      if (rc) return abandon(rc);
       in = mh;
     }
     std::vector<_Float16> ow(m->colprefix.back() * mh, static_cast<_Float16>(0.0f));
@@ -542,7 +556,7 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
       const size_t w2 = 2 * m->widths[b];
       const float* wt = tensor(key(b, m->mask_layers) + ".weight", w2 * mh);
       const float* bs = tensor(key(b, m->mask_layers) + ".bias", w2);
-      if (!wt || !bs) return fail(ANCHA_HIP_INVALID);
+      if (!wt || !bs) return missing(key(b, m->mask_layers) + ".*");
       for (size_t r = 0; r < w2; r++) {
         for (size_t e = 0; e < mh; e++)
           ow[(m->colprefix[b] + r) * mh + e] = static_cast<_Float16>(wt[r * mh + e]);
@@ -551,7 +565,7 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
     }
     rc = upload(ow, &h.ow);
     if (!rc) rc = upload(ob, &h.ob);
-    if (rc) return fail(rc);
+    if (rc) return abandon(rc);
   }
   // GLU gather tables (network.rs:248-263): covering (band, local bin) entries per FFT bin.
   {
@@ -580,10 +594,41 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
     if (!rc) rc = upload(base, &m->d_band_base);
     if (!rc) rc = upload(stride, &m->d_band_stride);
     if (!rc) rc = upload(width, &m->d_band_width);
-    if (rc) return fail(rc);
+    if (rc) return abandon(rc);
   }
-  rc = ensure_rope(m, c->chunk_samples / c->hop + 1);
-  if (rc) return fail(rc);
+  // Rotary and tile tables for the chunk's frame count (network.rs:280-299,331-332), built on
+  // the device from the checkpoint's frequencies.
+  {
+    m->frames = c->chunk_samples / c->hop + 1;
+    std::vector<float> freqs;
+    for (int axis = 0; axis < 2; axis++)
+      for (size_t i = 0; i < m->depth; i++) {
+        const std::vector<float>& f = m->freqs[2 * i + axis];
+        freqs.insert(freqs.end(), f.begin(), f.end());
+      }
+    const size_t ntiles = group_tiles(m, m->frames);
+    if (m->frames * kRopeFloats * m->depth > 0x7fffffff || ntiles > 0x7fffffff)
+      return abandon(ancha::fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_roformer_create: chunk too long"));
+    rc = upload(freqs, &m->d_freqs);
+    if (!rc) rc = alloc(m->depth * m->frames * kRopeFloats, &m->time_rope);
+    if (!rc) rc = alloc(m->depth * m->bands * kRopeFloats, &m->band_rope);
+    if (!rc) rc = alloc(ntiles, &m->d_group_of_tile);
+    if (!rc) rc = alloc(m->bands + 1, &m->d_group_first);
+    if (rc) return abandon(rc);
+    hipError_t e = ancha::launch_axis_rope(m->d_freqs, static_cast<int>(m->depth),
+                                           static_cast<int>(m->frames), m->time_rope, nullptr);
+    if (e == hipSuccess)
+      e = ancha::launch_axis_rope(m->d_freqs + m->depth * kHeadDim / 2,
+                                  static_cast<int>(m->depth), static_cast<int>(m->bands),
+                                  m->band_rope, nullptr);
+    if (e == hipSuccess)
+      e = ancha::launch_group_tiles(m->d_group_col0, static_cast<int>(m->bands),
+                                    static_cast<int>((m->frames + 127) / 128),
+                                    static_cast<long>(ntiles), m->d_group_of_tile,
+                                    m->d_group_first, nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (e != hipSuccess) return abandon(ancha::hip_fail(e, "ancha_hip_roformer_create"));
+  }
   *model = m;
   return ANCHA_HIP_OK;
 }
@@ -595,16 +640,22 @@ size_t ancha_hip_roformer_workspace(const ancha_hip_roformer* m, size_t frames) 
 
 int ancha_hip_roformer_forward(ancha_hip_roformer* m, const float* spectrum, size_t frames,
                                void* workspace, size_t workspace_bytes, float* masks,
-                               hipStream_t stream) {
-  if (!m) return ANCHA_HIP_INVALID;
+                               const volatile int* cancelled, hipStream_t stream) {
+  static const std::string kWhere = "ancha_hip_roformer_forward: ";
+  if (const int s = ancha::sticky()) return s;
+  if (!m) return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null model");
   if (frames == 0) return ANCHA_HIP_OK;
   if (!spectrum || !workspace || !masks || !aligned16(spectrum) || !aligned16(workspace) ||
       !aligned16(masks))
-    return ANCHA_HIP_INVALID;
-  if (workspace_bytes < ancha_hip_roformer_workspace(m, frames)) return ANCHA_HIP_INVALID;
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null or unaligned buffer");
+  if (frames > 0x7fffffff)
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "too many frames");
+  if (workspace_bytes < ancha_hip_roformer_workspace(m, frames))
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "workspace too small");
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev != m->device) return ANCHA_HIP_INVALID;
-  return forward_impl(m, &spectrum, 1, frames, workspace, &masks, stream);
+  if (hipGetDevice(&dev) != hipSuccess || dev != m->device)
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "called on another device than the model's");
+  return forward_impl(m, &spectrum, 1, frames, workspace, &masks, cancelled, nullptr, stream);
 }
 
 size_t ancha_hip_separate_workspace(const ancha_hip_roformer* m, size_t samples) {
@@ -612,19 +663,41 @@ size_t ancha_hip_separate_workspace(const ancha_hip_roformer* m, size_t samples)
   return separate_layout(m, samples).total;
 }
 
+namespace {
+
+// The first check flag in the order the reference runtime meets them, as its message.
+const char* flag_message(unsigned flags) {
+  if (flags & ancha::kFlagInput) return "non-finite STFT input";
+  if (flags & ancha::kFlagMasks) return "non-finite model output";
+  if (flags & ancha::kFlagIstftUncovered) return "iSTFT has an uncovered sample";
+  if (flags & ancha::kFlagChunk) return "non-finite chunk output";
+  return "uncovered overlap-add sample";
+}
+
+}  // namespace
+
 int ancha_hip_separate(ancha_hip_roformer* m, const float* audio, size_t samples, void* workspace,
                        size_t workspace_bytes, float* stems, float* residual,
-                       hipStream_t stream) {
-  if (!m) return ANCHA_HIP_INVALID;
+                       const volatile int* cancelled, hipStream_t stream) {
+  static const std::string kWhere = "ancha_hip_separate: ";
+  if (const int s = ancha::sticky()) return s;
+  if (!m) return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null model");
   if (samples == 0) return ANCHA_HIP_OK;
-  if (!audio || !workspace || !stems || !aligned16(workspace)) return ANCHA_HIP_INVALID;
-  if (residual && m->stems != 1) return ANCHA_HIP_INVALID;
-  if (workspace_bytes < ancha_hip_separate_workspace(m, samples)) return ANCHA_HIP_INVALID;
+  if (!audio || !workspace || !stems || !aligned16(workspace))
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null or unaligned buffer");
+  if (residual && m->stems != 1)
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "a residual needs a one-stem model");
+  if (samples > (size_t(1) << 40))
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "clip too long");
+  if (workspace_bytes < ancha_hip_separate_workspace(m, samples))
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "workspace too small");
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev != m->device) return ANCHA_HIP_INVALID;
+  if (hipGetDevice(&dev) != hipSuccess || dev != m->device)
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "called on another device than the model's");
   const Plan p = plan_for(m, samples);
   const SepLayout l = separate_layout(m, samples);
   unsigned char* ws = static_cast<unsigned char*>(workspace);
+  unsigned* flags = reinterpret_cast<unsigned*>(ws + l.flags);
   float* chunk = reinterpret_cast<float*>(ws + l.chunk);
   float* spectrum = reinterpret_cast<float*>(ws + l.spectrum);
   float* masks = reinterpret_cast<float*>(ws + l.masks);
@@ -632,12 +705,21 @@ int ancha_hip_separate(ancha_hip_roformer* m, const float* audio, size_t samples
   float* sums = reinterpret_cast<float*>(ws + l.sums);
   float* weights = reinterpret_cast<float*>(ws + l.weights);
   const long length = static_cast<long>(p.length), cs = static_cast<long>(m->chunk);
-  hipError_t e = ancha::launch_zero(sums, static_cast<long>(m->stems) * 2 * length, stream);
+  // On cancellation the work already enqueued still reads and writes the caller's buffers:
+  // wait for it, so the caller may release them on return.
+  auto cancel = [&]() {
+    (void)hipStreamSynchronize(stream);
+    return ancha::fail(ANCHA_HIP_CANCELLED, "task cancelled");
+  };
+  auto device_error = [&](hipError_t e) { return ancha::hip_fail(e, "ancha_hip_separate"); };
+  hipError_t e = ancha::launch_zero(reinterpret_cast<float*>(flags), 1, stream);
+  if (e == hipSuccess) e = ancha::launch_zero(sums, static_cast<long>(m->stems) * 2 * length, stream);
   if (e == hipSuccess) e = ancha::launch_zero(weights, length, stream);
-  if (e != hipSuccess) return -static_cast<int>(e);
+  if (e != hipSuccess) return device_error(e);
   const size_t mask_stride = 4 * m->fft_bins * p.frames;
   const size_t chunk_floats = 2 * m->chunk, spectrum_floats = p.frames * 4 * m->fft_bins;
   for (size_t i = 0; i < p.starts.size(); i += 2) {
+    if (cancel_requested(cancelled)) return cancel();  // runtime.rs:118
     const size_t nch = std::min<size_t>(2, p.starts.size() - i);
     const float* spectra[2];
     float* masks_of[2];
@@ -647,14 +729,17 @@ int ancha_hip_separate(ancha_hip_roformer* m, const float* audio, size_t samples
       float* chunk_c = chunk + c * chunk_floats;
       float* spectrum_c = spectrum + c * spectrum_floats;
       e = ancha::launch_chunk_gather(audio, static_cast<long>(samples), static_cast<long>(start),
-                                     static_cast<long>(p.border), remaining, cs, chunk_c, stream);
+                                     static_cast<long>(p.border), remaining, cs, chunk_c, flags,
+                                     stream);
       if (e == hipSuccess)
         e = ancha::launch_stft(chunk_c, cs, static_cast<int>(m->hop), spectrum_c, stream);
-      if (e != hipSuccess) return -static_cast<int>(e);
+      if (e != hipSuccess) return device_error(e);
       spectra[c] = spectrum_c;
       masks_of[c] = masks + c * m->stems * mask_stride;
     }
-    int rc = forward_impl(m, spectra, nch, p.frames, ws + l.model, masks_of, stream);
+    const int rc = forward_impl(m, spectra, nch, p.frames, ws + l.model, masks_of, cancelled,
+                                flags, stream);
+    if (rc == ANCHA_HIP_CANCELLED) return cancel();
     if (rc) return rc;
     // Overlap-add in chunk order, as one chunk at a time would.
     for (size_t c = 0; c < nch; c++) {
@@ -668,17 +753,25 @@ int ancha_hip_separate(ancha_hip_roformer* m, const float* audio, size_t samples
           e = ancha::launch_ola_accumulate(frames_buf, static_cast<int>(p.frames),
                                            static_cast<int>(m->hop), cs,
                                            static_cast<long>(start), length, first, last, s == 0,
-                                           sums + s * 2 * length, weights, stream);
-        if (e != hipSuccess) return -static_cast<int>(e);
+                                           sums + s * 2 * length, weights, flags, stream);
+        if (e != hipSuccess) return device_error(e);
       }
     }
   }
   for (size_t s = 0; s < m->stems; s++) {
     e = ancha::launch_finish(sums + s * 2 * length, weights, length, static_cast<long>(p.border),
                              static_cast<long>(samples), audio, stems + s * 2 * samples,
-                             s == 0 ? residual : nullptr, stream);
-    if (e != hipSuccess) return -static_cast<int>(e);
+                             s == 0 ? residual : nullptr, flags, stream);
+    if (e != hipSuccess) return device_error(e);
   }
+  // The reference checks every chunk's model output and audio as it goes (runtime.rs:172-176,
+  // chunk.rs:57-60,76-79); here the kernels set flags and the clip's one read-back reports them.
+  unsigned host_flags = 0;
+  e = hipMemcpyAsync(&host_flags, flags, sizeof(host_flags), hipMemcpyDeviceToHost, stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return device_error(e);
+  if (host_flags) return ancha::fail(ANCHA_HIP_INVALID, flag_message(host_flags));
+  if (cancel_requested(cancelled)) return ancha::fail(ANCHA_HIP_CANCELLED, "task cancelled");
   return ANCHA_HIP_OK;
 }
 
@@ -686,14 +779,19 @@ void ancha_hip_roformer_destroy(ancha_hip_roformer* m) { free_all(m); }
 
 int ancha_hip_stft(const float* signal, size_t samples, size_t hop, float* spectrum,
                    hipStream_t stream) {
+  static const std::string kWhere = "ancha_hip_stft: ";
+  if (const int s = ancha::sticky()) return s;
   if (samples == 0) return ANCHA_HIP_OK;
-  if (!signal || !spectrum || hop == 0 || hop > kFft / 2 || samples <= kFft / 2 ||
-      !aligned16(spectrum))
-    return ANCHA_HIP_INVALID;
-  if (samples / hop + 1 > 0x7fffffff) return ANCHA_HIP_UNSUPPORTED;
-  const hipError_t e = ancha::launch_stft(signal, static_cast<long>(samples),
-                                          static_cast<int>(hop), spectrum, stream);
-  return e == hipSuccess ? 0 : -static_cast<int>(e);
+  if (!signal || !spectrum || !aligned16(spectrum))
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null or unaligned buffer");
+  if (hop == 0 || hop > kFft / 2 || samples <= kFft / 2)
+    return ancha::fail(ANCHA_HIP_INVALID,
+                       kWhere + "hop outside (0, 1024] or input not longer than FFT/2");
+  if (samples / hop + 1 > 0x7fffffff || samples > (size_t(1) << 40))
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "too many frames");
+  return ancha::hip_status(ancha::launch_stft(signal, static_cast<long>(samples),
+                                              static_cast<int>(hop), spectrum, stream),
+                           "ancha_hip_stft");
 }
 
 size_t ancha_hip_istft_workspace(size_t frames) { return frames * 2 * kFft * sizeof(float); }
@@ -701,12 +799,18 @@ size_t ancha_hip_istft_workspace(size_t frames) { return frames * 2 * kFft * siz
 int ancha_hip_istft(const float* spectrum, const float* masks, size_t frames, size_t hop,
                     size_t length, int zero_dc, void* workspace, size_t workspace_bytes,
                     float* out, hipStream_t stream) {
+  static const std::string kWhere = "ancha_hip_istft: ";
+  if (const int s = ancha::sticky()) return s;
   if (frames == 0 || length == 0) return ANCHA_HIP_OK;
-  if (!spectrum || !masks || !workspace || !out || hop == 0 || hop > kFft / 2)
-    return ANCHA_HIP_INVALID;
-  if (length + kFft / 2 > (frames - 1) * hop + kFft) return ANCHA_HIP_INVALID;
+  if (!spectrum || !masks || !workspace || !out)
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "null buffer");
+  if (hop == 0 || hop > kFft / 2) return ancha::fail(ANCHA_HIP_INVALID, kWhere + "hop outside (0, 1024]");
+  if (frames > 0x7fffffff || length > (size_t(1) << 40))
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, kWhere + "too many frames");
+  if (length + kFft / 2 > (frames - 1) * hop + kFft)
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "requested length exceeds frame support");
   if (workspace_bytes < ancha_hip_istft_workspace(frames) || !aligned16(workspace))
-    return ANCHA_HIP_INVALID;
+    return ancha::fail(ANCHA_HIP_INVALID, kWhere + "workspace too small or unaligned");
   float* frames_buf = static_cast<float*>(workspace);
   const long n = static_cast<long>(length);
   hipError_t e = ancha::launch_zero(out, 2 * n, stream);
@@ -716,8 +820,8 @@ int ancha_hip_istft(const float* spectrum, const float* masks, size_t frames, si
   // One chunk covering the whole output: unit fade weights (first and last).
   if (e == hipSuccess)
     e = ancha::launch_ola_accumulate(frames_buf, static_cast<int>(frames), static_cast<int>(hop),
-                                     n, 0, n, true, true, false, out, nullptr, stream);
-  return e == hipSuccess ? 0 : -static_cast<int>(e);
+                                     n, 0, n, true, true, false, out, nullptr, nullptr, stream);
+  return ancha::hip_status(e, "ancha_hip_istft");
 }
 
 }  // extern "C"

@@ -14,6 +14,7 @@ from typing import Optional
 import torch
 
 from . import _native
+from ._tensors import require, require_optional
 
 ATTENTION_HEAD_DIM = 64
 
@@ -49,11 +50,11 @@ def _rows(t: torch.Tensor) -> tuple[torch.Tensor, int]:
     return flat, flat.stride(1)
 
 
-def _table(rope: Optional[torch.Tensor], tokens: int) -> Optional[torch.Tensor]:
+def _table(rope: Optional[torch.Tensor], tokens: int,
+           device: torch.device) -> Optional[torch.Tensor]:
     if rope is None:
         return None
-    if tuple(rope.shape) != (4, tokens, ATTENTION_HEAD_DIM) or rope.dtype != torch.float32:
-        raise ValueError("rotary table must be float32 [4, tokens, 64]")
+    require(rope, "rotary table", device, (4, tokens, ATTENTION_HEAD_DIM))
     return rope.contiguous()
 
 
@@ -69,9 +70,11 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         return None
     if not q.is_cuda or not available():
         return None
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        require(t, name, q.device)
     groups, tokens, heads, _ = q.shape
     (qf, ldq), (kf, ldk), (vf, ldv) = (_rows(t) for t in (q, k, v))
-    table = _table(rope, tokens)
+    table = _table(rope, tokens, q.device)
     out = torch.empty((groups, tokens, heads, ATTENTION_HEAD_DIM), device=q.device,
                       dtype=torch.float32)
     rc = _native.lib().ancha_hip_attention(
@@ -89,11 +92,12 @@ def gated_attention(packed: torch.Tensor, heads: int,
         return None
     if not packed.is_cuda or not available():
         return None
+    require(packed, "packed", packed.device)
     groups, tokens, columns = packed.shape
     flat, ld = _rows(packed)
     if ld != columns:
         flat, ld = flat.contiguous(), columns
-    table = _table(rope, tokens)
+    table = _table(rope, tokens, packed.device)
     out = torch.empty((groups, tokens, heads, ATTENTION_HEAD_DIM), device=packed.device,
                       dtype=torch.float32)
     rc = _native.lib().ancha_hip_gated_attention(
@@ -120,9 +124,8 @@ def linear_supported(k: int, m: int) -> bool:
     return k > 0 and k % 8 == 0 and m > 0 and m % 128 == 0
 
 
-def _matrix(t: torch.Tensor, name: str) -> torch.Tensor:
-    if t.dim() != 2 or t.dtype != torch.float32 or not t.is_cuda:
-        raise ValueError(f"{name} must be a float32 CUDA matrix")
+def _matrix(t: torch.Tensor, name: str, device: torch.device) -> torch.Tensor:
+    require(t, name, device)
     return t if t.stride(1) == 1 else t.contiguous()
 
 
@@ -150,8 +153,12 @@ def _linear(x: torch.Tensor, weight: torch.Tensor, epilogue: Epilogue,
         residual = residual.contiguous()
     if not x.is_cuda or not available():
         return None
-    x = _matrix(x, "x")
-    w = _matrix(weight, "weight").contiguous()
+    x = _matrix(x, "x", x.device)
+    w = _matrix(weight, "weight", x.device).contiguous()
+    require_optional(epilogue.bias, "bias", x.device, (m,))
+    require_optional(residual, "residual", x.device, (n, m))
+    if table is not None:
+        require(table, "rotary table", x.device)
     bias = None if epilogue.bias is None else epilogue.bias.contiguous()
     out = torch.empty((n, m), device=x.device, dtype=torch.float32)
     fn = _native.lib().ancha_hip_norm_linear if norm else _native.lib().ancha_hip_linear
@@ -180,9 +187,10 @@ def unit_norm(x: torch.Tensor, scale: Optional[torch.Tensor] = None) -> torch.Te
     x / max(||x||_2, 1e-12) over the last axis, times ``scale``."""
     if x.dtype != torch.float32 or not x.is_cuda:
         raise ValueError("unit_norm takes a float32 CUDA tensor")
+    dim = x.shape[-1]
+    require_optional(scale, "scale", x.device, (dim,))
     if not available():
         raise RuntimeError("the gfx950 kernels cannot run on this device")
-    dim = x.shape[-1]
     flat = x.reshape(-1, dim)
     if flat.stride(1) != 1:
         flat = flat.contiguous()

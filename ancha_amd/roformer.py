@@ -15,6 +15,7 @@ import numpy as np
 import torch
 
 from . import _native
+from ._tensors import require
 from .workload import axis_rope_packed
 
 WEIGHT_NAMES = ("attn_gamma", "to_qkv", "to_gates", "to_gates_bias", "to_out", "ff_gamma",
@@ -57,9 +58,11 @@ class Transformer:
     def forward(self, x: torch.Tensor, rope: torch.Tensor) -> torch.Tensor:
         """x [groups, tokens, dim] float32 on the block's device; rope the [4, tokens, 64]
         table of this axis. Returns a new [groups, tokens, dim] tensor."""
+        if x.dim() != 3:
+            raise ValueError("x must be [groups, tokens, dim]")
         groups, tokens, dim = x.shape
-        if dim != self.dim or tuple(rope.shape) != (4, tokens, 64):
-            raise ValueError("x / rope shapes do not match the block")
+        require(x, "x", self.device, (groups, tokens, self.dim))
+        require(rope, "rope", self.device, (4, tokens, 64))
         x = x.contiguous()
         rope = rope.contiguous()
         need = self.workspace_bytes(groups * tokens)
@@ -115,10 +118,12 @@ class AxisPair:
 
     def forward(self, x: torch.Tensor, time_rope: torch.Tensor,
                 band_rope: torch.Tensor) -> torch.Tensor:
+        if x.dim() != 4:
+            raise ValueError("x must be [batch, bands, frames, dim]")
         batch, bands, frames, dim = x.shape
-        if dim != self.time.dim or tuple(time_rope.shape) != (4, frames, 64) \
-                or tuple(band_rope.shape) != (4, bands, 64):
-            raise ValueError("x / rope shapes do not match the blocks")
+        require(x, "x", self.time.device, (batch, bands, frames, self.time.dim))
+        require(time_rope, "time_rope", self.time.device, (4, frames, 64))
+        require(band_rope, "band_rope", self.time.device, (4, bands, 64))
         x = x.contiguous()
         lib = _native.lib()
         need = int(lib.ancha_hip_axis_pair_workspace(self.time._handle, self.band._handle,

@@ -17,6 +17,7 @@ import numpy as np
 import torch
 
 from . import _native
+from ._tensors import require
 from .plan import AttentionPlan, backend_plan, require_gpu_kernels, run_settings
 
 N_FFT = 2048
@@ -44,6 +45,42 @@ _TensorFn = ctypes.CFUNCTYPE(ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p, 
 
 def _stream(device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
+
+
+class CancelFlag:
+    """The reference's ``cancelled: &AtomicBool`` (runtime.rs:118, network.rs:334,367): an int
+    the C ABI reads between chunk pairs, layer pairs and mask heads. ``set()`` may be called
+    from another thread while a forward or separation runs."""
+
+    def __init__(self):
+        self._flag = ctypes.c_int(0)
+
+    def set(self) -> None:
+        self._flag.value = 1
+
+    def is_set(self) -> bool:
+        return self._flag.value != 0
+
+    def pointer(self):
+        return ctypes.byref(self._flag)
+
+
+def _flag(cancelled: Optional[CancelFlag]):
+    return None if cancelled is None else cancelled.pointer()
+
+
+def check_spectrum(spectrum: torch.Tensor, device) -> None:
+    """The model input: float32 [frames, 4*1025] on ``device``."""
+    if spectrum.dim() != 2 or spectrum.shape[1] != 4 * BINS:
+        raise ValueError("spectrum must be [frames, 4100]")
+    require(spectrum, "spectrum", device)
+
+
+def check_audio(audio: torch.Tensor, device) -> None:
+    """Stereo audio: float32 [2, samples] on ``device``."""
+    if audio.dim() != 2 or audio.shape[0] != 2:
+        raise ValueError("audio must be [2, samples]")
+    require(audio, "audio", device)
 
 
 class Roformer:
@@ -105,28 +142,29 @@ class Roformer:
             self._ws = torch.empty(need, dtype=torch.uint8, device=self.device)
         return self._ws
 
-    def forward(self, spectrum: torch.Tensor) -> torch.Tensor:
+    def forward(self, spectrum: torch.Tensor,
+                cancelled: Optional[CancelFlag] = None) -> torch.Tensor:
         """spectrum [frames, 4*1025] float32 (frame, bin*2 + channel, re/im) ->
-        masks [stems, 2*1025, 2, frames]."""
+        masks [stems, 2*1025, 2, frames]. Raises ``Cancelled`` when ``cancelled`` is set."""
+        check_spectrum(spectrum, self.device)
         frames = spectrum.shape[0]
-        if spectrum.dim() != 2 or spectrum.shape[1] != 4 * BINS:
-            raise ValueError("spectrum must be [frames, 4100]")
         spectrum = spectrum.contiguous()
         lib = _native.lib()
         ws = self._workspace(int(lib.ancha_hip_roformer_workspace(self._handle, frames)))
         masks = torch.empty((self.stems, 2 * BINS, 2, frames), device=self.device)
         _native.check(lib.ancha_hip_roformer_forward(self._handle, spectrum.data_ptr(), frames,
                                                      ws.data_ptr(), ws.numel(), masks.data_ptr(),
-                                                     _stream(self.device)))
+                                                     _flag(cancelled), _stream(self.device)))
         return masks
 
     __call__ = forward
 
-    def separate(self, audio: torch.Tensor):
+    def separate(self, audio: torch.Tensor, cancelled: Optional[CancelFlag] = None):
         """Stereo audio [2, samples] float32 on the device -> (stems [stems, 2, samples],
-        residual [2, samples] for one-stem models else None)."""
-        if audio.dim() != 2 or audio.shape[0] != 2:
-            raise ValueError("audio must be [2, samples]")
+        residual [2, samples] for one-stem models else None). Raises ``ValueError`` with the
+        reference runtime's message for non-finite input, model or chunk output, and
+        ``Cancelled`` when ``cancelled`` is set."""
+        check_audio(audio, self.device)
         audio = audio.contiguous()
         n = audio.shape[1]
         lib = _native.lib()
@@ -136,7 +174,7 @@ class Roformer:
         _native.check(lib.ancha_hip_separate(self._handle, audio.data_ptr(), n, ws.data_ptr(),
                                              ws.numel(), stems.data_ptr(),
                                              None if residual is None else residual.data_ptr(),
-                                             _stream(self.device)))
+                                             _flag(cancelled), _stream(self.device)))
         return stems, residual
 
     def close(self) -> None:
@@ -154,6 +192,7 @@ class Roformer:
 def stft(signal: torch.Tensor, hop: int) -> torch.Tensor:
     """Stft::forward of both channels of signal [2, samples] -> [frames, 1025, 2, 2]
     (frame, bin, channel, re/im)."""
+    check_audio(signal, signal.device)
     signal = signal.contiguous()
     n = signal.shape[1]
     out = torch.empty((n // hop + 1, BINS, 2, 2), device=signal.device)
@@ -165,7 +204,11 @@ def stft(signal: torch.Tensor, hop: int) -> torch.Tensor:
 def istft(spectrum: torch.Tensor, masks: torch.Tensor, hop: int, length: int,
           zero_dc: bool = False) -> torch.Tensor:
     """Stft::inverse of spectrum * masks (masks [2*1025, 2, frames]) -> [2, length]."""
+    if spectrum.dim() != 4:
+        raise ValueError("spectrum must be [frames, 1025, 2, 2]")
     frames = spectrum.shape[0]
+    require(spectrum, "spectrum", spectrum.device, (frames, BINS, 2, 2))
+    require(masks, "masks", spectrum.device, (2 * BINS, 2, frames))
     spectrum, masks = spectrum.contiguous(), masks.contiguous()
     lib = _native.lib()
     ws = torch.empty(int(lib.ancha_hip_istft_workspace(frames)), dtype=torch.uint8,

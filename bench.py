@@ -9,7 +9,10 @@ inputs resident in HBM.
 
 Prints ONE JSON line: throughput in TFLOP/s (4*G*H*T^2*d per call), the live roofline of the
 attention kernel (HIP events over the timed region on the launch stream) and the restated
-reference CPU path (the oracle's materialized-tile attention) timed on the host's cores.
+reference CPU path (the oracle's materialized-tile attention) timed on the host's cores. The
+same line carries, under "mel_roformer", the second half of the headline metric: the
+audio-seconds per second of the Mel-RoFormer separation of a 30 s clip (as `--workload mel`
+measures it, with its own roofline and CPU baseline).
 
 `--workload band` measures the band-axis op [1602, 60, 8, 64] instead (HBM-bound roofline),
 `--workload layer` one RoFormer layer pair on [2, 60, 801, 384], and `--workload mel` the
@@ -267,12 +270,27 @@ SEPARATIONS = {
 }
 
 
+# The reference's own published CPU speed on this model (Flex backend, batched), for context
+# beside the restated CPU path: one 3 s clip (301 frames) in 6.21 s total (5.12 s model) on an
+# Intel i5-12400 (6 cores / 12 threads), docs/reports/derur-benchmark.json:930-939.
+REFERENCE_CPU_MEL = {"value": round(3.0 / 6.21, 4), "unit": "audio-s/s", "cores": 12,
+                     "sample": "Mel-Karaoke, one 3 s clip (301 frames): 6.21 s total, 5.12 s "
+                               "model, i5-12400 6C/12T (docs/reports/derur-benchmark.json:930-939)"}
+
+
 def run_separation(args, torch, dev) -> int:
+    result = separation_result(args.workload, args.steps, args.warmup, args.no_cpu_baseline,
+                               torch, dev)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def separation_result(workload, steps, warmup, no_cpu_baseline, torch, dev) -> dict:
     """Separation of a stereo clip resident in HBM with a bundled config and random
     N(0, 0.02) weights: Mel-Karaoke on 30 s (`mel`) or BS-RoFormer-large on 5 min (`bs`)."""
     from ancha_amd import separation as S
     from ancha_amd import workload as W
-    name, seconds, metric, described = SEPARATIONS[args.workload]
+    name, seconds, metric, described = SEPARATIONS[workload]
     config = S.load_config(name)
     sr = config["sample_rate"]
     n = seconds * sr
@@ -283,32 +301,32 @@ def run_separation(args, torch, dev) -> int:
     audio = torch.from_numpy(audio_np).to(dev)
     step = lambda: model.separate(audio)
     out = step()
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         out = step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         out = step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(end) / args.steps
+    gpu_ms = start.elapsed_time(end) / steps
     step_ = config["chunk_samples"] // config["overlap"]
     border = config["chunk_samples"] - step_
     border = border if n > 2 * border else 0
     chunks = len(range(0, n + 2 * border, step_))
     flops = chunks * mel_flops(config)
     achieved = flops / (gpu_ms * 1e-3) / 1e12
-    log(f"{args.workload} separation: {gpu_ms:.1f} ms per {seconds} s clip ({chunks} chunks), "
+    log(f"{workload} separation: {gpu_ms:.1f} ms per {seconds} s clip ({chunks} chunks), "
         f"{seconds / (gpu_ms * 1e-3):.1f} audio-s/s, {achieved:.1f} TFLOP/s")
     result = {
         "metric": metric,
-        "value": round(seconds * args.steps / wall, 3),
-        "unit": "audio-s/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 3), "higher_is_better": True,
+        "value": round(seconds * steps / wall, 3),
+        "unit": "audio-s/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 3), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": f"synthetic: seeded pink noise + 3 sines, {seconds} s stereo 44.1 kHz; weights "
                 "N(0,0.02), gamma 1, rotary theta 10000 (seeded)",
@@ -321,11 +339,11 @@ def run_separation(args, torch, dev) -> int:
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
                      "traffic": None, "scope": "whole separation (all kernels)"},
     }
-    if not args.no_cpu_baseline:
+    if not no_cpu_baseline:
         import oracle.mel as OM
         threads = cpu_threads()
         weights = OM.weights_from_tensors(config, tensors)
-        if args.workload == "mel":
+        if workload == "mel":
             log(f"timing the restated reference CPU path on the first chunk ({threads} threads)")
             t0 = time.perf_counter()
             OM.separate(audio_np, config, weights, threads=threads, chunks=1)
@@ -353,9 +371,11 @@ def run_separation(args, torch, dev) -> int:
                       f"{config['depth']} and credited {seconds}/{chunks} s of audio")
         result["cpu_baseline"] = {"value": round(value, 5), "unit": "audio-s/s",
                                   "cores": threads, "kind": "port", "sample": sample}
+        if workload == "mel":
+            result["cpu_baseline"]["reference_published"] = REFERENCE_CPU_MEL
     del out
-    print(json.dumps(result), flush=True)
-    return 0
+    model.close()
+    return result
 
 
 def main() -> int:
@@ -370,6 +390,11 @@ def main() -> int:
                     help="sequence length of the time / band op workloads (default 801 / 60); "
                          "for length sweeps, the headline uses the default")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-mel", action="store_true",
+                    help="time workload: leave out the Mel-RoFormer 30 s separation section")
+    ap.add_argument("--mel-steps", type=int, default=5,
+                    help="timed clips of the Mel-RoFormer section of the time workload")
+    ap.add_argument("--mel-warmup", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="time a plain device copy of the workload's I/O size instead; its "
                          "FETCH_SIZE / WRITE_SIZE counters calibrate the HBM traffic figures")
@@ -470,6 +495,13 @@ def main() -> int:
         log("timing the restated reference CPU path")
         result["cpu_baseline"] = cpu_baseline(q.cpu().numpy(), k.cpu().numpy(),
                                               v.cpu().numpy(), table_np, out.cpu().numpy())
+    if args.workload == "time" and not args.no_mel:
+        # The second half of the headline metric: audio-seconds/sec of the Mel-RoFormer
+        # separation of a 30 s clip, in the same JSON line.
+        del q, k, v, out
+        log("Mel-RoFormer separation of a 30 s clip")
+        result["mel_roformer"] = separation_result("mel", args.mel_steps, args.mel_warmup,
+                                                   args.no_cpu_baseline, torch, dev)
     print(json.dumps(result), flush=True)
     return 0
 

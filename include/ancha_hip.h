@@ -4,10 +4,11 @@
  * Drop-in replacement for the CUDA-only entry points of Ancha's op boundary
  * `ancha_models::fused` (crates/ancha-models/src/fused/mod.rs). Each function below names the
  * reference item it replaces. All tensors are caller-owned device buffers of fp32 values,
- * row-major, with explicit row strides in elements; the library writes only `out` and
- * allocates no device memory per call. Every call is stream-ordered on `stream` (0 = the
- * null stream), does not synchronise the host and is safe to call from several host threads
- * on different streams.
+ * row-major, with explicit row strides in elements; the library writes only `out` (and the
+ * caller's workspace) and allocates no device memory per call (the *_create calls allocate
+ * a model's weights once). Every call is stream-ordered on `stream` (0 = the null stream),
+ * does not synchronise the host (except ancha_hip_separate, once at its end, and *_create)
+ * and is safe to call from several host threads on different streams.
  *
  * Return codes:
  *   ANCHA_HIP_OK (0)            success (launched on `stream`).
@@ -17,9 +18,12 @@
  *   ANCHA_HIP_INVALID (2)       arguments break the op contract (the reference's `assert!`
  *                               panics inside `launch`): null pointers, column ranges that do
  *                               not fit the row stride, ...; nothing was launched.
+ *   ANCHA_HIP_CANCELLED (3)     the caller's cancellation flag was set (the reference's "task
+ *                               cancelled", src/runtime.rs:118; network.rs:334,367).
  *   < 0                         a HIP runtime error, -(hipError_t). The failure is sticky, like
  *                               the reference's `device::check` (src/device.rs:11-41): every
- *                               later call returns it again without launching anything.
+ *                               later call of any entry point returns it again without
+ *                               launching anything.
  * ancha_hip_last_error() describes the most recent non-zero return of the calling thread.
  */
 #ifndef ANCHA_HIP_H
@@ -37,6 +41,7 @@ typedef struct ihipStream_t *hipStream_t;
 #define ANCHA_HIP_OK 0
 #define ANCHA_HIP_UNSUPPORTED 1
 #define ANCHA_HIP_INVALID 2
+#define ANCHA_HIP_CANCELLED 3
 
 /* Head width the attention kernels are specialised for.
  * Replaces `pub const ATTENTION_HEAD_DIM: usize = 64` (fused/mod.rs:18). */
@@ -197,12 +202,17 @@ size_t ancha_hip_roformer_workspace(const ancha_hip_roformer *model, size_t fram
 
 /* masks [stems][2 * 1025][re, im][frames] = model(spectrum [frames][1025][channel][re, im]):
  * band split -> axis loop (the frequency pass reads the time layout in place) -> mask heads
- * (tanh hidden layers, GLU, overlapping-band average). The first call with a new frame count
- * builds that count's rotary tables (device allocation); other calls allocate nothing.
+ * (tanh hidden layers, GLU, overlapping-band average). Allocates nothing and does not wait:
+ * the rotary tables of the chunk's frame count are built at create time, those of any other
+ * frame count in the workspace by the call itself. Calls sharing a model may run concurrently
+ * on different streams with different workspaces.
+ * `cancelled` (or NULL): checked before each layer pair and each mask head like the reference's
+ * `&AtomicBool`; a set flag returns ANCHA_HIP_CANCELLED, and the work already enqueued on
+ * `stream` still runs (synchronise it before releasing the buffers).
  * Replaces `Roformer::forward` (network.rs:303-400). */
 int ancha_hip_roformer_forward(ancha_hip_roformer *model, const float *spectrum, size_t frames,
                                void *workspace, size_t workspace_bytes, float *masks,
-                               hipStream_t stream);
+                               const volatile int *cancelled, hipStream_t stream);
 
 /* Device bytes of the workspace ancha_hip_separate needs for a clip of `samples` samples. */
 size_t ancha_hip_separate_workspace(const ancha_hip_roformer *model, size_t samples);
@@ -210,11 +220,17 @@ size_t ancha_hip_separate_workspace(const ancha_hip_roformer *model, size_t samp
 /* stems [stems][2][samples] (and, for one-stem models, residual [2][samples] = audio - stem, or
  * NULL) from stereo audio [2][samples], all device memory: reflect-bordered chunks every
  * chunk_samples / overlap samples, STFT, forward, complex masks, iSTFT, fade-weighted
- * overlap-add, border crop. Allocates nothing.
+ * overlap-add, border crop. Allocates nothing. The reference runtime's checks run on the
+ * device and are read back once, at the end (the call waits for `stream` there): a
+ * non-finite input sample, model output or chunk output, or an uncovered iSTFT / overlap-add
+ * sample returns ANCHA_HIP_INVALID with the reference's message (runtime.rs:172-176;
+ * crates/ancha-audio/src/dsp.rs:57-60,126-131; chunk.rs:57-60,76-79); the stems are then not
+ * valid. `cancelled` (or NULL) is checked before each pair of chunks, each layer pair and each
+ * mask head; a set flag returns ANCHA_HIP_CANCELLED after the enqueued work has finished.
  * Replaces the chunk loop of src/runtime.rs:103-238 (+ residual_audio, :403-420). */
 int ancha_hip_separate(ancha_hip_roformer *model, const float *audio, size_t samples,
                        void *workspace, size_t workspace_bytes, float *stems, float *residual,
-                       hipStream_t stream);
+                       const volatile int *cancelled, hipStream_t stream);
 
 void ancha_hip_roformer_destroy(ancha_hip_roformer *model);
 

@@ -87,3 +87,83 @@ def layer_case():
         else:
             w[name] = W.normal(shape, W.SEED_WEIGHTS + i, 0.02)
     return w, W.normal(LAYER_SHAPE, 4)
+
+
+# Tiny networks at the reference's kernel_package scale (tests/support/mod.rs:18-55): dim 128,
+# 2 heads of 64, FF x4, a 101-frame chunk. Mel: two stems, three overlapping bands (the
+# coverage average), mask depth 2 = two tanh hidden layers. BS: one stem, three bands that
+# partition the bins, a final norm, mask depth 2 = one hidden layer (every Linear counted).
+NETWORKS = ("mel", "bs")
+NETWORK_ROWS = np.arange(0, 2050, 11)        # mask rows kept in the fixture
+NETWORK_FRAMES = np.arange(0, 101, 5)        # frames kept in the fixture
+
+
+def network_config(name):
+    config = {"family": "mel-band-roformer" if name == "mel" else "bs-roformer", "dim": 128,
+              "depth": 2, "heads": 2, "head_dim": 64, "ff_mult": 4, "mask_depth": 2,
+              "mask_expansion": 1, "sample_rate": 44100, "n_fft": 2048, "hop": 441,
+              "chunk_samples": 44100, "overlap": 2, "zero_dc": True,
+              "stems": ["vocals", "instrumental"] if name == "mel" else ["vocals"]}
+    if name == "mel":
+        config["bands"] = [list(range(0, 400)), list(range(300, 900)), list(range(625, 1025))]
+    else:
+        config["bands"] = [list(range(0, 300)), list(range(300, 700)), list(range(700, 1025))]
+    return config
+
+
+def network_case(name):
+    """(config, checkpoint tensors, packed spectrum [101, 4100]). Weights N(0, 0.05^2) from
+    the seeded stream; every gamma 1 + 0.3 wave(...) (not 1, so a dropped gamma shows); the
+    rotary frequencies of layer i, axis a use theta = 10000 / (1 + 2i + a) (so a table built
+    from the wrong layer's frequencies shows)."""
+    config = network_config(name)
+    tensors = W.roformer_tensors(config, seed=W.SEED_WEIGHTS + (7 if name == "mel" else 8),
+                                 scale=0.05)
+    for i, key in enumerate(sorted(k for k in tensors if k.endswith("gamma"))):
+        tensors[key] = (np.float32(1.0) + np.float32(0.3) * wave(tensors[key].shape, 0.37 * i))
+    for key in tensors:
+        if key.endswith("rotary_embed.freqs"):
+            i, axis = int(key.split(".")[1]), int(key.split(".")[2])
+            tensors[key] = W.rope_freqs(64, 10000.0 / (1 + 2 * i + axis))
+    spectrum = wave((101, 4100), 0.7 if name == "mel" else 1.9) * np.float32(2.0)
+    return config, tensors, spectrum
+
+
+def moments(a):
+    """Float64 sum, sum of squares and position-weighted sum of a whole output."""
+    a = np.asarray(a, np.float64).ravel()
+    return np.array([a.sum(), (a * a).sum(), (a * (np.arange(a.size) % 89 + 1)).sum()])
+
+
+# The two full-size models at their production chunk shapes, random-init N(0, 0.02^2) weights
+# (gammas 1, theta 10000), one chunk of seeded audio through the oracle's STFT:
+#   mel_karaoke_d6: Mel-Karaoke (60 overlapping bands, dim 384), depth 6, 801 frames;
+#   bs_large_d2:    BS-RoFormer-large (62 bands, dim 512, mask MLP x4), depth 2, 1101 frames.
+PRODUCTION = {
+    "mel_karaoke_d6": ("mel_karaoke", 6, 51, 52),
+    "bs_large_d2": ("bs_roformer_large", 2, 53, 54),
+}
+PRODUCTION_ROW_STEP, PRODUCTION_FRAME_STEP = 41, 16
+
+
+def production_config(name):
+    from ancha_amd import separation as S
+    bundled, depth, _, _ = PRODUCTION[name]
+    return dict(S.load_config(bundled), depth=depth)
+
+
+def production_case(name, device=None):
+    """(config, checkpoint tensors, packed spectrum [frames, 4100]); with a torch `device`
+    the weight stream is generated there (same values)."""
+    import oracle.mel as M
+    config = production_config(name)
+    _, _, seed, audio_seed = PRODUCTION[name]
+    tensors = W.roformer_tensors(config, seed=seed, device=device)
+    chunk = W.audio(config["chunk_samples"], seed=audio_seed)
+    spectrum = M.pack_spectra([M.stft(chunk[c], config["n_fft"], config["hop"])
+                               for c in range(2)])
+    return config, tensors, spectrum
+
+
+def production_index(frames):
+    return np.arange(0, 2050, PRODUCTION_ROW_STEP), np.arange(0, frames, PRODUCTION_FRAME_STEP)

@@ -81,3 +81,58 @@ def test_fixtures_reject_a_planted_mistake():
     bad[3] = np.abs(bad[3])
     err = np.abs(O.attention_op(q, k, v, rope=bad)[0][np.ix_(rows, heads)] - f["band"]).max()
     assert err > 1e-4
+
+
+@pytest.mark.parametrize("name", C.NETWORKS)
+def test_network_forward(name):
+    """The oracle's network end (band split, axis loop, final norm, mask heads with GLU and the
+    overlapping-band average) against the torch float64 restatement of Roformer::forward in
+    tests/golden/make_golden.py, with non-zero weights, non-unit gammas and per-layer rotary
+    frequencies."""
+    import oracle.mel as M
+    f = fixture("network.npz")
+    config, tensors, spectrum = C.network_case(name)
+    np.testing.assert_allclose(C.checksum(spectrum, *(tensors[k] for k in sorted(tensors))),
+                               f[f"checksum_{name}"], rtol=1e-12)
+    got = M.model_forward(spectrum, config, M.weights_from_tensors(config, tensors), threads=4)
+    want = f[name]
+    sub = got[:, C.NETWORK_ROWS][..., C.NETWORK_FRAMES]
+    close(sub, want, 1e-5 * float(np.abs(want).max()))
+    np.testing.assert_allclose(C.moments(got), f[f"moments_{name}"], rtol=1e-4)
+
+
+def test_network_fixture_rejects_planted_mistakes():
+    """Mistakes a restatement of network.rs could plausibly make each move the masks far
+    outside the fixture's tolerance: counting Mel mask depth like BS (one hidden layer fewer),
+    swapping the GLU halves, and skipping the overlapping-band average."""
+    import oracle.mel as M
+    f = fixture("network.npz")
+    config, tensors, spectrum = C.network_case("mel")
+    want = f["mel"]
+    scale = float(np.abs(want).max())
+
+    def masks(cfg, weights):
+        out = M.model_forward(spectrum, cfg, weights, threads=4)
+        return out[:, C.NETWORK_ROWS][..., C.NETWORK_FRAMES]
+
+    weights = M.weights_from_tensors(config, tensors)
+    # GLU halves swapped: value <-> gate rows of every band's output projection.
+    swapped = dict(weights, masks=[
+        {"hidden": h["hidden"],
+         "out": [(np.concatenate([w[w.shape[0] // 2:], w[:w.shape[0] // 2]]),
+                  np.concatenate([b[b.shape[0] // 2:], b[:b.shape[0] // 2]])) for w, b in h["out"]]}
+        for h in weights["masks"]])
+    assert np.abs(masks(config, swapped) - want).max() > 1e-2 * scale
+    # One hidden layer dropped (the BS count applied to a Mel network).
+    shallow = dict(weights, masks=[{"hidden": h["hidden"][:1], "out": h["out"]}
+                                   for h in weights["masks"]])
+    fewer = dict(config, mask_depth=1)
+    assert np.abs(masks(fewer, shallow) - want).max() > 1e-2 * scale
+    # Sum instead of average over the covering bands: rows 2*300.. are covered twice.
+    got = M.model_forward(spectrum, config, weights, threads=4)
+    cover = np.zeros(2050)
+    for band in config["bands"]:
+        for fb in band:
+            cover[2 * fb:2 * fb + 2] += 1
+    summed = got * cover[None, :, None, None]
+    assert np.abs(summed[:, C.NETWORK_ROWS][..., C.NETWORK_FRAMES] - want).max() > 1e-2 * scale

@@ -3,24 +3,23 @@ forward (band split, axis loop, mask heads) and the chunked separation, against 
 Bounds: the DSP is fp32 end to end (relative 1e-5 of the signal scale); the network runs its
 GEMMs and attention on fp16 operands, so masks and stems are compared by SNR, with the 50 dB
 end-to-end gate of the separated stems."""
+import os
+
 import numpy as np
 import pytest
 import torch
 
 import oracle.mel as M
+from ancha_amd import _native
 from ancha_amd import separation as S
 from ancha_amd import workload as W
+from tests.golden import cases as C
 
 from .test_mel_oracle import identity_model, tiny_config
 
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
 pytestmark = pytest.mark.gpu
-
-
-@pytest.fixture(scope="module")
-def gpu():
-    if not torch.cuda.is_available():
-        pytest.skip("no GPU")
-    return torch.device("cuda:0")
 
 
 def snr_db(ref, got):
@@ -186,3 +185,192 @@ def test_separate_mel_karaoke_one_layer_pair(gpu):
     db = snr_db(want[0], stems[0].cpu().numpy())
     report("mel-karaoke depth-1 separation stem SNR dB", db)
     assert db > 50.0
+
+
+def fixture(name):
+    return np.load(os.path.join(GOLDEN, name), allow_pickle=False)
+
+
+@pytest.mark.parametrize("name", C.NETWORKS)
+def test_forward_matches_network_golden(gpu, name):
+    """Tiny Mel / BS networks with non-zero weights, non-unit gammas and per-layer rotary
+    frequencies against the committed torch float64 restatement (tests/golden/network.npz)."""
+    config, tensors, spectrum = C.network_case(name)
+    f = fixture("network.npz")
+    np.testing.assert_allclose(C.checksum(spectrum, *(tensors[k] for k in sorted(tensors))),
+                               f[f"checksum_{name}"], rtol=1e-12)
+    model = S.Roformer(config, tensors, gpu)
+    got = model(torch.from_numpy(spectrum).to(gpu)).cpu().numpy()
+    db = snr_db(f[name], got[:, C.NETWORK_ROWS][..., C.NETWORK_FRAMES])
+    report(f"network {name} vs golden SNR dB", db)
+    assert db > 50.0
+    m = C.moments(got)
+    want = f[f"moments_{name}"]
+    assert abs(m[1] - want[1]) < 1e-3 * want[1]
+
+
+@pytest.mark.parametrize("name", sorted(C.PRODUCTION))
+def test_forward_production_shapes_match_oracle(gpu, name):
+    """Mel-Karaoke at depth 6 on one 801-frame chunk and BS-RoFormer-large at depth 2 on one
+    1101-frame chunk against the oracle's masks (tests/golden/production_networks.npz, a
+    row/frame lattice of them plus whole-output moments)."""
+    config, tensors, spectrum = C.production_case(name, device=gpu)
+    f = fixture("production_networks.npz")
+    np.testing.assert_allclose(C.checksum(spectrum, *(tensors[k] for k in sorted(tensors))),
+                               f[f"checksum_{name}"], rtol=1e-12)
+    model = S.Roformer(config, tensors, gpu)
+    got = model(torch.from_numpy(spectrum).to(gpu)).cpu().numpy()
+    rows, frames = C.production_index(spectrum.shape[0])
+    db = snr_db(f[name], got[:, rows][..., frames])
+    report(f"{name} forward vs oracle SNR dB", db)
+    assert db > 50.0
+    m, want = C.moments(got), f[f"moments_{name}"]
+    report(f"{name} sum of squares rel. diff", abs(m[1] - want[1]) / want[1])
+    assert abs(m[1] - want[1]) < 1e-3 * want[1]
+    model.close()
+
+
+def composed_separation(model, audio, config):
+    """The chunk loop of runtime.rs:103-238 written out on the host from the library's single
+    pieces (GPU STFT, one-chunk forward, masked iSTFT) and the oracle's overlap-add: the
+    reference against which the fused ancha_hip_separate (two chunks per forward, GPU
+    overlap-add) is checked."""
+    n = audio.shape[1]
+    cs, hop = config["chunk_samples"], config["hop"]
+    step = cs // config["overlap"]
+    border = cs - step if n > 2 * (cs - step) else 0
+    length = n + 2 * border
+    stems = len(config["stems"])
+    acc = M.OverlapAdd(stems * 2, length, cs)
+    for start in range(0, length, step):
+        remaining = min(length - start, cs)
+        i = np.arange(cs)
+        local = np.where(i < remaining, i, M._reflect(i, remaining))
+        chunk = audio[:, M._reflect(start + local - border, n)]
+        if remaining <= cs // 2:
+            chunk[:, remaining:] = 0.0
+        spec = S.stft(torch.from_numpy(np.ascontiguousarray(chunk)).to(model.device), hop)
+        masks = model(spec.reshape(spec.shape[0], -1))
+        planes = []
+        for s in range(stems):
+            y = S.istft(spec, masks[s], hop, cs, config["zero_dc"]).cpu().numpy()
+            planes += [y[0], y[1]]
+        acc.add(start, planes)
+    return acc.finish().reshape(stems, 2, length)[..., border:border + n]
+
+
+def check_separation(model, config, audio, gpu, label):
+    """Properties of a full-size separation plus equality with the composed chunk loop."""
+    x = torch.from_numpy(audio).to(gpu)
+    stems, residual = model.separate(x)
+    again, _ = model.separate(x)
+    torch.cuda.synchronize()
+    assert torch.isfinite(stems).all()
+    assert torch.equal(stems, again), "separation must be deterministic"
+    got = stems.cpu().numpy()
+    assert np.abs(got).max() > 1e-4, "stems must not be silent"
+    if residual is not None:
+        np.testing.assert_allclose(residual.cpu().numpy(), audio - got[0], atol=1e-6)
+    want = composed_separation(model, audio, config)
+    db = snr_db(want, got)
+    report(f"{label}: fused separation vs composed chunk loop SNR dB", db)
+    assert db > 60.0
+
+
+def test_mel_karaoke_depth6_30s_separation(gpu):
+    """BASELINE's Mel-RoFormer workload: Mel-Karaoke at depth 6 on a 30 s clip (21 overlapping
+    801-frame chunks, run two at a time through the model)."""
+    config = S.load_config("mel_karaoke")
+    tensors = W.roformer_tensors(config, seed=55, device=gpu)
+    model = S.Roformer(config, tensors, gpu)
+    check_separation(model, config, W.audio(30 * 44100, seed=56), gpu, "mel-karaoke 30 s")
+    model.close()
+
+
+def test_bs_large_two_chunks_batched(gpu):
+    """BS-RoFormer-large at depth 2: a clip of exactly two 1101-frame chunks goes through the
+    model as one batch of two."""
+    config = dict(S.load_config("bs_roformer_large"), depth=2)
+    tensors = W.roformer_tensors(config, seed=57, device=gpu)
+    model = S.Roformer(config, tensors, gpu)
+    check_separation(model, config, W.audio(config["chunk_samples"], seed=58), gpu,
+                     "bs-large depth 2, two chunks")
+    model.close()
+
+
+def test_bs_large_depth12_separation(gpu):
+    """BS-RoFormer-large as configured (depth 12) on a 60 s clip."""
+    config = S.load_config("bs_roformer_large")
+    tensors = W.roformer_tensors(config, seed=59, device=gpu)
+    model = S.Roformer(config, tensors, gpu)
+    check_separation(model, config, W.audio(60 * 44100, seed=60), gpu, "bs-large depth 12, 60 s")
+    model.close()
+
+
+def test_forward_other_frame_count(gpu):
+    """A frame count other than the chunk's: rotary and tile tables built in the workspace."""
+    config = tiny_config(depth=2)
+    tensors = W.roformer_tensors(config, seed=61)
+    model = S.Roformer(config, tensors, gpu)
+    weights = M.weights_from_tensors(config, tensors)
+    for samples in (66_150, 20_000):
+        spec = packed_spectrum(W.audio(samples, seed=62), config["hop"])
+        got = model(torch.from_numpy(spec).to(gpu)).cpu().numpy()
+        want = M.model_forward(spec, config, weights, threads=8)
+        db = snr_db(want, got)
+        report(f"tiny forward at {spec.shape[0]} frames masks SNR dB", db)
+        assert db > 50.0
+
+
+def test_separate_reports_non_finite_input(gpu):
+    config = tiny_config(stems=("vocals",))
+    model = S.Roformer(config, W.roformer_tensors(config, seed=63), gpu)
+    audio = W.audio(60_000, seed=64)
+    audio[1, 12_345] = np.nan
+    with pytest.raises(ValueError, match="non-finite STFT input"):
+        model.separate(torch.from_numpy(audio).to(gpu))
+    audio[1, 12_345] = 0.0
+    stems, _ = model.separate(torch.from_numpy(audio).to(gpu))
+    assert torch.isfinite(stems).all()
+    assert _native.lib().ancha_hip_check() == 0
+
+
+def test_separate_reports_non_finite_model_output(gpu):
+    config = tiny_config(stems=("vocals",))
+    tensors = W.roformer_tensors(config, seed=65)
+    tensors["mask_estimators.0.to_freqs.1.0.4.bias"][7] = np.inf
+    model = S.Roformer(config, tensors, gpu)
+    with pytest.raises(ValueError, match="non-finite model output"):
+        model.separate(torch.from_numpy(W.audio(60_000, seed=66)).to(gpu))
+
+
+def test_cancelled_separation_and_forward(gpu):
+    config = tiny_config(stems=("vocals",))
+    model = S.Roformer(config, W.roformer_tensors(config, seed=67), gpu)
+    flag = S.CancelFlag()
+    audio = torch.from_numpy(W.audio(60_000, seed=68)).to(gpu)
+    model.separate(audio, cancelled=flag)
+    flag.set()
+    with pytest.raises(_native.Cancelled, match="task cancelled"):
+        model.separate(audio, cancelled=flag)
+    spec = torch.from_numpy(packed_spectrum(W.audio(44_100, seed=69), config["hop"])).to(gpu)
+    with pytest.raises(_native.Cancelled):
+        model(spec, cancelled=flag)
+    torch.cuda.synchronize()
+    assert _native.lib().ancha_hip_check() == 0
+
+
+def test_wrappers_reject_host_and_misshaped_tensors(gpu):
+    config = tiny_config(stems=("vocals",))
+    model = S.Roformer(config, W.roformer_tensors(config, seed=70), gpu)
+    with pytest.raises(ValueError):
+        model.separate(torch.zeros((2, 50_000)))                       # host memory
+    with pytest.raises(ValueError):
+        model.separate(torch.zeros((2, 50_000), dtype=torch.float64, device=gpu))
+    with pytest.raises(ValueError):
+        model(torch.zeros((101, 4100), device=gpu, dtype=torch.float16))
+    spec = S.stft(torch.zeros((2, 5000), device=gpu), 441)
+    with pytest.raises(ValueError):
+        S.istft(spec, torch.zeros((2050, 2, spec.shape[0] - 1), device=gpu), 441, 4000)
+    with pytest.raises(ValueError):
+        S.istft(spec, torch.zeros((2050, 2, spec.shape[0])), 441, 4000)

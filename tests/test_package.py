@@ -141,14 +141,12 @@ def test_bundled_configs_validate():
 
 
 @pytest.mark.gpu
-def test_kernel_package_loads_and_matches_oracle(tmp_path):
+def test_kernel_package_loads_and_matches_oracle(tmp_path, gpu):
     """kernel_package (tests/support/mod.rs:17-25) written, loaded and run on the GPU."""
     import torch
 
     import oracle.mel as M
 
-    if not torch.cuda.is_available():
-        pytest.skip("no GPU")
     config = tiny_package_config(kernel=True)
     tensors = write_package(str(tmp_path), config)
     model, manifest = P.load_model(str(tmp_path), torch.device("cuda:0"))
