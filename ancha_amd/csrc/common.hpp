@@ -39,10 +39,13 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// True for +-inf and NaN. A bit test: the library is compiled with -fno-honor-nans, under which
-// isfinite() may fold to true.
+// True for +-inf and NaN. The library is compiled with -fno-honor-nans, under which the
+// compiler folds isfinite() and even an exponent bit test on a float to an infinity compare
+// (NaN assumed absent); the empty asm hides the value's float origin, so the bit test stays.
 __device__ __forceinline__ bool non_finite(float x) {
-  return (__builtin_bit_cast(unsigned, x) & 0x7f800000u) == 0x7f800000u;
+  unsigned bits = __builtin_bit_cast(unsigned, x);
+  asm volatile("" : "+v"(bits));
+  return (bits & 0x7f800000u) == 0x7f800000u;
 }
 
 // ORs `bit` into the device check word (a vector-memory atomic).
