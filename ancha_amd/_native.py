@@ -60,6 +60,7 @@ SIGNATURES = {
     "ancha_hip_stft": (_int, [_p, _sz, _sz, _p, _p]),
     "ancha_hip_istft_workspace": (_sz, [_sz]),
     "ancha_hip_istft": (_int, [_p, _p, _sz, _sz, _sz, _int, _p, _sz, _p, _p]),
+    "ancha_hip_istft_noalloc": (_int, [_p, _p, _sz, _sz, _sz, _int, _p, _p]),
     "ancha_hip_check": (_int, []),
     "ancha_hip_last_error": (ctypes.c_char_p, []),
 }

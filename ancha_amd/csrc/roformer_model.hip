@@ -15,6 +15,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -822,6 +823,60 @@ int ancha_hip_istft(const float* spectrum, const float* masks, size_t frames, si
     e = ancha::launch_ola_accumulate(frames_buf, static_cast<int>(frames), static_cast<int>(hop),
                                      n, 0, n, true, true, false, out, nullptr, nullptr, stream);
   return ancha::hip_status(e, "ancha_hip_istft");
+}
+
+// ------------------------------------------------------------------------------------------
+// Allocation-free iSTFT: ancha_hip_istft with its frame workspace in a static device array.
+// ------------------------------------------------------------------------------------------
+
+}  // extern "C"
+
+namespace {
+
+// The windowed inverse frames [frames][2][2048] of one ancha_hip_istft_noalloc call. Every GPU
+// the library runs on holds its own copy (24 MiB) until the process ends. Host code uses only
+// the per-device address from hipGetSymbolAddress, never this name.
+constexpr size_t kIstftScratchFrames = 1536;
+__device__ __align__(256) float scratch[kIstftScratchFrames * 2 * kFft];
+
+constexpr int kScratchDevices = 64;
+std::mutex g_scratch_mutex;
+float* g_scratch[kScratchDevices] = {};
+
+// The current device's address of `scratch`, looked up on the first call on that device.
+int scratch_address(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_istft_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kScratchDevices)
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_istft_noalloc: device index >= 64");
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_istft_noalloc: hipGetSymbolAddress");
+    g_scratch[dev] = static_cast<float*>(ptr);
+  }
+  *out = g_scratch[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ancha_hip_istft_noalloc(const float* spectrum, const float* masks, size_t frames, size_t hop,
+                            size_t length, int zero_dc, float* out, hipStream_t stream) {
+  static const std::string kWhere = "ancha_hip_istft_noalloc: ";
+  if (const int s = ancha::sticky()) return s;
+  if (frames == 0 || length == 0) return ANCHA_HIP_OK;
+  if (frames > kIstftScratchFrames)
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED,
+                       kWhere + "more than 1536 frames (the static scratch holds 1536)");
+  float* ws = nullptr;
+  if (const int rc = scratch_address(&ws)) return rc;
+  return ancha_hip_istft(spectrum, masks, frames, hop, length, zero_dc, ws,
+                         ancha_hip_istft_workspace(frames), out, stream);
 }
 
 }  // extern "C"

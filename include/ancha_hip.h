@@ -248,6 +248,15 @@ int ancha_hip_istft(const float *spectrum, const float *masks, size_t frames, si
                     size_t length, int zero_dc, void *workspace, size_t workspace_bytes,
                     float *out, hipStream_t stream);
 
+/* ancha_hip_istft without a workspace argument, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). No counterpart in the reference.
+ * The inverse frames go to a static device array of the library (24 MiB per GPU, held until
+ * the process ends), so `frames` is at most 1536 (ANCHA_HIP_UNSUPPORTED beyond, with a
+ * message). Allocates nothing. Calls that overlap on one GPU (other streams or threads) share
+ * that array and race: serialise them. Results equal ancha_hip_istft's. */
+int ancha_hip_istft_noalloc(const float *spectrum, const float *masks, size_t frames, size_t hop,
+                            size_t length, int zero_dc, float *out, hipStream_t stream);
+
 /* Sticky device-failure check: 0, or the first HIP error (< 0) any call has met.
  * Replaces `device::check()` (src/device.rs:30-41) for this path. */
 int ancha_hip_check(void);
