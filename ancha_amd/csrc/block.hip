@@ -36,6 +36,9 @@ struct ancha_hip_block {
   _Float16* ff_out_w;  // [dim, hidden]
   float* ff_out_b;     // [dim]
   float* out_scale;    // [dim] sqrt(dim)*output_gamma, or null
+  // Fragment-major copies for the fused tail (tail.hip), or null where it does not apply:
+  // W_out^T, W1'^T and W2^T (the last two with their k axis in kPerm16 order).
+  _Float16 *wo_frag = nullptr, *w1_frag = nullptr, *w2_frag = nullptr;
 };
 
 namespace {
@@ -71,6 +74,25 @@ int upload(const std::vector<T>& host, T** dev) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Fragment-major copy of W^T [rows][k] (k contiguous) for the A operand of the 32x32x16 MFMA
+// in tail.hip: fragment (b, s) is 512 halves at (b * (k / 16) + s) * 512, lane l's 8 at 8 l,
+// holding W^T[32 b + l % 32][16 s + perm(8 (l / 32) + t)] for t < 8, perm = kPerm16 (or the
+// identity). rows % 32 == 0, k % 16 == 0.
+std::vector<_Float16> fragment_major(const std::vector<_Float16>& wt, size_t rows, size_t k,
+                                     bool permute) {
+  std::vector<_Float16> out(rows * k);
+  const size_t steps = k / 16;
+  for (size_t b = 0; b < rows / 32; b++)
+    for (size_t s = 0; s < steps; s++)
+      for (size_t l = 0; l < 64; l++)
+        for (size_t t = 0; t < 8; t++) {
+          const size_t kk = 8 * (l / 32) + t;
+          const size_t src = 16 * s + (permute ? static_cast<size_t>(ancha::kPerm16[kk]) : kk);
+          out[((b * steps + s) * 64 + l) * 8 + t] = wt[(32 * b + l % 32) * k + src];
+        }
+  return out;
+}
 
 // One block GEMM through the fp16-weight kernel.
 int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, size_t m,
@@ -189,6 +211,26 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
   }
   e = ancha::launch_attention(ap, true, stream);
   if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_block_forward");
+  if (b->w1_frag) {
+    // Out projection, residual, norm, feed-forward (hidden activation on chip), residual and
+    // the optional output norm in one kernel.
+    ancha::TailParams tp{};
+    tp.attended = attended;
+    tp.x = x;
+    tp.wo = b->wo_frag;
+    tp.w1 = b->w1_frag;
+    tp.b1 = b->ff_in_b;
+    tp.w2 = b->w2_frag;
+    tp.b2 = b->ff_out_b;
+    tp.out_scale = b->out_scale;
+    tp.out = out;
+    tp.xh = b->out_scale && xh_out ? xh : nullptr;
+    tp.rows = static_cast<int>(rows);
+    tp.dim = static_cast<int>(dim);
+    tp.inner = static_cast<int>(inner);
+    tp.hidden = static_cast<int>(b->hidden);
+    return ancha::hip_status(ancha::launch_block_tail(tp, stream), "ancha_hip_block_forward");
+  }
   // x1 = x + attended . W_out
   rc = gemm(attended, true, rows, inner, b->out_w, dim, nullptr, false, nullptr, 0, 1, 0, x, x1,
             false, false, stream);
@@ -309,6 +351,12 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
   if (!rc) rc = upload(w2, &b->ff_out_w);
   if (!rc) rc = upload(b2, &b->ff_out_b);
   if (!rc) rc = upload(os, &b->out_scale);
+  if (!rc && ancha::block_tail_supported(static_cast<int>(dim), static_cast<int>(inner),
+                                         static_cast<int>(hidden))) {
+    rc = upload(fragment_major(ow, dim, inner, false), &b->wo_frag);
+    if (!rc) rc = upload(fragment_major(w1, hidden, dim, true), &b->w1_frag);
+    if (!rc) rc = upload(fragment_major(w2, dim, hidden, true), &b->w2_frag);
+  }
   if (rc) {
     ancha_hip_block_destroy(b);
     return rc;
@@ -352,7 +400,9 @@ void ancha_hip_block_destroy(ancha_hip_block* b) {
   for (void* p : {static_cast<void*>(b->packed_w), static_cast<void*>(b->packed_b),
                   static_cast<void*>(b->out_w), static_cast<void*>(b->ff_in_w),
                   static_cast<void*>(b->ff_in_b), static_cast<void*>(b->ff_out_w),
-                  static_cast<void*>(b->ff_out_b), static_cast<void*>(b->out_scale)})
+                  static_cast<void*>(b->ff_out_b), static_cast<void*>(b->out_scale),
+                  static_cast<void*>(b->wo_frag), static_cast<void*>(b->w1_frag),
+                  static_cast<void*>(b->w2_frag)})
     if (p) (void)hipFree(p);
   delete b;
 }

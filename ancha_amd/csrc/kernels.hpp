@@ -118,6 +118,33 @@ struct Gemm16Params {
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream);
 
+// Fused tail of the RoFormer block (tail.hip), 128 rows per workgroup step:
+//   x1 = x + attended . W_out; h = fp16(GELU(fp16(unit_norm(x1)) . W1' + b1));
+//   out = x1 + h . W2 + b2; with out_scale: out = unit_norm(out) * out_scale and, with xh,
+//   xh = fp16(unit_norm(out)).
+// attended fp16 [rows][inner]; x, out fp32 [rows][dim] (out may be x); xh fp16 [rows][dim].
+// wo, w1, w2: fp16 fragment-major copies of W_out^T [dim][inner], W1'^T [hidden][dim] and
+// W2^T [dim][hidden] (tail_fragments), the last two with their k axis in kPerm16 order.
+struct TailParams {
+  const _Float16* attended;
+  const float* x;
+  const _Float16* wo;
+  const _Float16* w1;
+  const float* b1;
+  const _Float16* w2;
+  const float* b2;
+  const float* out_scale;  // [dim] or null
+  float* out;
+  _Float16* xh;            // or null (needs out_scale)
+  int rows, dim, inner, hidden;
+};
+bool block_tail_supported(int dim, int inner, int hidden);
+hipError_t launch_block_tail(const TailParams& p, hipStream_t stream);
+
+// Order of k within each 16-block of a fragment-major weight whose B operand comes straight
+// from another product's accumulators (tail.hip): B k-slot 8h + t holds feature kPerm16[8h + t].
+constexpr int kPerm16[16] = {0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15};
+
 // Axis pair of two blocks (block.hip) whose output norms hand the next block its fp16 operand:
 // xh_in, the workspace holds fp16(unit_norm(x)) from the previous pair; xh_out, the band block
 // leaves fp16(unit_norm(out)) there for the next pair (which must satisfy block_chainable with
