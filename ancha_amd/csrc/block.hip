@@ -39,6 +39,8 @@ struct ancha_hip_block {
   // Fragment-major copies for the fused tail (tail.hip), or null where it does not apply:
   // W_out^T, W1'^T and W2^T (the last two with their k axis in kPerm16 order).
   _Float16 *wo_frag = nullptr, *w1_frag = nullptr, *w2_frag = nullptr;
+  // Fragment-major copy of the packed projection for qkv.hip, or null.
+  _Float16* packed_frag = nullptr;
 };
 
 namespace {
@@ -182,8 +184,26 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
     e = ancha::launch_norm_half(x, static_cast<int>(rows), static_cast<int>(dim), nullptr,
                                 nullptr, xh, stream);
   if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_block_forward");
-  int rc = gemm(xh, true, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
-                split ? split : 1, inner, nullptr, packed, true, false, stream, kLog2eHost);
+  int rc = 0;
+  if (b->packed_frag) {
+    ancha::QkvParams qp{};
+    qp.xh = xh;
+    qp.w = b->packed_frag;
+    qp.bias = b->packed_b;
+    qp.rope = rope;
+    qp.out = packed;
+    qp.rows = static_cast<int>(rows);
+    qp.dim = static_cast<int>(dim);
+    qp.cols = static_cast<int>(b->columns);
+    qp.tokens = static_cast<int>(tokens);
+    qp.token_div = static_cast<int>(split ? split : 1);
+    qp.width = static_cast<int>(inner);
+    qp.q_scale = kLog2eHost;
+    rc = ancha::hip_status(ancha::launch_qkv(qp, stream), "ancha_hip_block_forward");
+  } else {
+    rc = gemm(xh, true, rows, dim, b->packed_w, b->columns, b->packed_b, false, rope, tokens,
+              split ? split : 1, inner, nullptr, packed, true, false, stream, kLog2eHost);
+  }
   if (rc) return rc;
   // attended = softmax(q k^T) v * sigmoid(gate), stored fp16.
   ancha::AttnParams ap{};
@@ -357,6 +377,8 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
     if (!rc) rc = upload(fragment_major(w1, hidden, dim, true), &b->w1_frag);
     if (!rc) rc = upload(fragment_major(w2, dim, hidden, true), &b->w2_frag);
   }
+  if (!rc && ancha::qkv_supported(static_cast<int>(dim), static_cast<int>(columns)))
+    rc = upload(fragment_major(pw, columns, dim, false), &b->packed_frag);
   if (rc) {
     ancha_hip_block_destroy(b);
     return rc;
@@ -402,7 +424,7 @@ void ancha_hip_block_destroy(ancha_hip_block* b) {
                   static_cast<void*>(b->ff_in_b), static_cast<void*>(b->ff_out_w),
                   static_cast<void*>(b->ff_out_b), static_cast<void*>(b->out_scale),
                   static_cast<void*>(b->wo_frag), static_cast<void*>(b->w1_frag),
-                  static_cast<void*>(b->w2_frag)})
+                  static_cast<void*>(b->w2_frag), static_cast<void*>(b->packed_frag)})
     if (p) (void)hipFree(p);
   delete b;
 }

@@ -141,6 +141,24 @@ struct TailParams {
 bool block_tail_supported(int dim, int inner, int hidden);
 hipError_t launch_block_tail(const TailParams& p, hipStream_t stream);
 
+// Packed q | k | v | gate projection of the block (qkv.hip): out fp16 [rows][cols] =
+// bias + xh . W with the rotary epilogue on columns [0, 2 width) (token of row r:
+// (r / token_div) % tokens; the packed [4, tokens, 64] table's key half is read, the query half
+// being it times 1/8) and the query columns times q_scale. xh fp16 [rows][dim]; w: fp16
+// fragment-major W^T [cols][dim] (natural k order, tail_fragments layout).
+struct QkvParams {
+  const _Float16* xh;
+  const _Float16* w;
+  const float* bias;   // [cols]
+  const float* rope;   // or null
+  _Float16* out;
+  int rows, dim, cols;
+  int tokens, token_div, width;
+  float q_scale;
+};
+bool qkv_supported(int dim, int cols);
+hipError_t launch_qkv(const QkvParams& p, hipStream_t stream);
+
 // Order of k within each 16-block of a fragment-major weight whose B operand comes straight
 // from another product's accumulators (tail.hip): B k-slot 8h + t holds feature kPerm16[8h + t].
 constexpr int kPerm16[16] = {0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15};

@@ -1,4 +1,4 @@
-// Fused tail of the RoFormer block on gfx950: everything after the attention core, 128 rows at
+// Fused tail of the RoFormer block on gfx950: everything after the attention core, 64 rows at
 // a time, with the feed-forward hidden activation kept on chip (crates/ancha-models/src/
 // roformer.rs:487-519, Transformer::forward_kernels after its gated_attention call):
 //   x1 = x + attended . W_out                          out projection + residual
@@ -19,11 +19,11 @@
 // kPerm16 at load time. So x1 -> unit_norm -> fp16 and h -> fp16 go from accumulators to B
 // fragments in LDS with one 16-byte store per lane and no shuffles.
 //
-// Workgroup: 8 waves, one per (row half rh, feature quarter fq); waves (0, fq) and (1, fq) share
-// a SIMD and read the same weight fragments, the second mostly from L1. The out accumulator
-// (128 rows x dim) stays in registers from the residual load to the final store; the hidden
-// dimension runs in chunks of 128 (per chunk: FF-in for 32 hidden units per wave, GELU, the
-// chunk's fp16 activation to LDS, then its FF-out contribution).
+// Workgroup: 64 rows, 4 waves, one per feature quarter (and SIMD); two workgroups per CU, whose
+// phases drift apart, so one's GELU / norm VALU work runs beside the other's MFMAs. The out
+// accumulator (64 rows x dim) stays in registers from the residual load to the final store; the
+// hidden dimension runs in chunks of 128 (per chunk: FF-in for 32 hidden units per wave, GELU,
+// the chunk's fp16 activation to LDS, then its FF-out contribution).
 #include "buffer.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
@@ -34,9 +34,9 @@ namespace {
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kRows = 128;        // rows per workgroup step
+constexpr int kRows = 64;         // rows per workgroup step
 constexpr int kChunk = 128;       // hidden units per chunk
-constexpr int kWaves = 8;
+constexpr int kWaves = 4;         // one per feature quarter (and per SIMD)
 constexpr int kFrag = 1024;       // bytes of one 32 x 16 fp16 fragment
 
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
@@ -77,7 +77,7 @@ __device__ __forceinline__ void row_totals(float* red, const float (&part)[NJ], 
 
 // DIM = 128 * NI features, INNER = heads * 64.
 template <int NI, int INNER>
-__global__ __launch_bounds__(kWaves * 64, 1) void block_tail_kernel(TailParams p) {
+__global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p) {
   constexpr int DIM = 128 * NI;
   constexpr int S0 = INNER / 16;   // k steps of the out projection
   constexpr int SD = DIM / 16;     // k steps of FF in
@@ -92,7 +92,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void block_tail_kernel(TailParams p
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int rh = wave >> 2, fq = wave & 3;
+  constexpr int rh = 0;  // the workgroup's 64 rows are one pair of 32-row blocks
+  const int fq = wave;
   const int half = lane >> 5, col = lane & 31;
   const int hidden = p.hidden, chunks = hidden / kChunk;
   const unsigned lane16 = (unsigned)lane * 16;
@@ -115,7 +116,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void block_tail_kernel(TailParams p
 
     // ---- the attended tile, straight into LDS as B fragments: fragment f = (jb, s) holds
     // rows 32 jb + (l % 32), k 16 s + 8 (l / 32) .. + 7 in lane order.
-    for (int f = wave; f < 4 * S0; f += kWaves) {
+    for (int f = wave; f < 2 * S0; f += kWaves) {
       const int jb = f / S0, s = f % S0;
       const unsigned off = ((unsigned)(32 * jb + col) * INNER + 16 * s + 8 * half) * 2;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
@@ -392,7 +393,7 @@ hipError_t launch_block_tail(const TailParams& p, hipStream_t stream) {
       cus <= 0)
     cus = 256;
   const int blocks = (p.rows + kRows - 1) / kRows;
-  const int grid = blocks < cus ? blocks : cus;
+  const int grid = blocks < 2 * cus ? blocks : 2 * cus;  // two workgroups per CU
   const int ni = p.dim / 128;
   if (p.inner == 512) {
     switch (ni) {
