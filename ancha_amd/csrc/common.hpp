@@ -37,6 +37,29 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
                                                 __builtin_bit_cast(h16x8, b), c, 0, 0, 0);
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// D(32x32 fp32) += A(32x16 fp16) . B(16x32 fp16).
+// Lane l holds A[row l%32][k 8*(l/32)..+7], B[k 8*(l/32)..+7][col l%32] and, in element
+// 4q + e, D[row 8q + 4*(l/32) + e][col l%32].
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h16x8, a),
+                                                __builtin_bit_cast(h16x8, b), c, 0, 0, 0);
+}
+
+// Zero accumulator for the first mfma32 of a chain, built in registers behind an empty asm so
+// that the compiler cannot fold it into the MFMA's inline-constant C operand. In that form the
+// compiler may give the MFMA a destination overlapping its A or B registers, and the 8-pass
+// MFMA then overwrites operand registers it has not finished reading (wrong products, varying
+// from run to run). A register C is tied to the destination, which keeps it apart from A and B.
+__device__ __forceinline__ f32x16 mfma32_zero() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; i++) z[i] = 0.f;
+  asm volatile("" : "+v"(z));
+  return z;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // True for +-inf and NaN. The library is compiled with -fno-honor-nans, under which the

@@ -20,16 +20,9 @@
 namespace ancha {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 constexpr int kRows = 128;
 constexpr int kWaves = 8;
 constexpr int kFrag = 1024;
-
-__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h16x8, a),
-                                                __builtin_bit_cast(h16x8, b), c, 0, 0, 0);
-}
 
 // SD = dim / 16 k steps.
 template <int SD>
@@ -94,9 +87,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
       const unsigned char* X = lds + opaque;
       f32x16 acc[4];
 #pragma unroll
-      for (int j = 0; j < 4; j++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[j][r] = 0.f;
+      for (int j = 0; j < 4; j++) acc[j] = mfma32_zero();
       // This block's bias columns (used after the K loop).
       float4 bias[4];
 #pragma unroll

@@ -32,24 +32,11 @@
 namespace ancha {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kRows = 64;         // rows per workgroup step
 constexpr int kChunk = 128;       // hidden units per chunk
 constexpr int kWaves = 4;         // one per feature quarter (and per SIMD)
 constexpr int kFrag = 1024;       // bytes of one 32 x 16 fp16 fragment
-
-__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(h16x8, a),
-                                                __builtin_bit_cast(h16x8, b), c, 0, 0, 0);
-}
-
-__device__ __forceinline__ f32x16 zero16() {
-  f32x16 z;
-#pragma unroll
-  for (int i = 0; i < 16; i++) z[i] = 0.f;
-  return z;
-}
 
 // Lane l's B fragment (8 halves) from accumulator values 8 sub .. 8 sub + 7 (q = 2 sub, 2 sub + 1).
 __device__ __forceinline__ u32x4 pack_frag(const f32x16& d, int sub, float s) {
@@ -204,7 +191,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
     // ---- feed-forward, 128 hidden units per chunk.
     for (int c = 0; c < chunks; c++) {
       // FF in: this wave's 32 hidden units 128 c + 32 fq + (8 q + 4 h + e).
-      f32x16 hacc[2] = {zero16(), zero16()};
+      f32x16 hacc[2] = {mfma32_zero(), mfma32_zero()};
       {
         constexpr int PD = 8;
         const int blk1 = 4 * c + fq;
