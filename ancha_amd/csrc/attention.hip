@@ -13,8 +13,10 @@
 // All global traffic goes through raw buffer loads/stores whose hardware range check returns 0
 // for rows at or past `tokens` (and drops stores there), so ragged tails need no branches.
 //
-//  * attention_time_kernel: long sequences (the time axis, T ~ 801). One workgroup = 8 waves x
-//    64 queries of one (group, head); 64-key K / V^T tiles are staged in LDS as fp16 (K rotated
+//  * attention_time_kernel: long sequences whose rows are not 16-byte aligned (aligned ones,
+//    every call the library itself makes, go to attention_long.hip's 32x32x16 kernel). One
+//    workgroup = 8 waves x 64 queries of one (group, head); 64-key K / V^T tiles are staged in
+//    LDS as fp16 (K rotated
 //    on the way), double buffered, the next tile's loads in flight while the current one is
 //    multiplied. The online softmax rescales lazily: the running maximum only moves when a
 //    tile exceeds it by more than kTau, so most tiles skip the O / l rescale.
@@ -23,22 +25,12 @@
 //    coalesced row loads, then each wave takes 16 queries; softmax is exact (one key tile).
 #include <type_traits>
 
-#include "buffer.hpp"
-#include "common.hpp"
-#include "kernels.hpp"
+#include "attention.hpp"
 
 namespace ancha {
 
-// Lazy-rescale threshold in log2 units: unnormalised probabilities stay below 2^kTau (fp16-safe).
-constexpr float kTau = 8.0f;
-// s_waitcnt operand (GFX9 encoding) waiting for all vector memory operations: vmcnt(0),
-// expcnt and lgkmcnt left at their maxima.
-constexpr int kWaitVmem = 0x0F70;
 // fp16 1.0 in both halves of a dword: the A operand of the row-sum MFMA.
 constexpr unsigned kOnesH2 = 0x3C003C00u;
-
-// Byte offset of 16-byte chunk c (8 fp16 channels) of K row r in a [64][64] fp16 tile.
-__device__ __forceinline__ int k_offset(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
 
 // Chunked V^T tile (time kernel): row d holds the 64 keys of channel d, and the 16-byte chunk
 // ks*4 + grp holds keys ks*32 + {grp*4 + i, 16 + grp*4 + i} (i = 0..3) in that order, so one
@@ -60,37 +52,6 @@ __device__ __forceinline__ u32x4 p_fragment(f32x4 a, f32x4 b) {
 // Dword j (keys a, b of channel j) of a V^T chunk from the fp16 channels 4c .. 4c+3 of two keys.
 __device__ __forceinline__ unsigned v_pair(u32x2 a, u32x2 b, int j) {
   return __builtin_amdgcn_perm(b[j >> 1], a[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
-}
-
-// First row of group g (token 0) in q/k/v/gate/out; token t adds t * p.tstep rows.
-__device__ __forceinline__ long group_row(const AttnParams& p, int g) {
-  return (long)(g / p.gsplit) * p.gouter + (long)(g % p.gsplit) * p.gstep;
-}
-
-// Output rows of one (group, head): [tokens, heads*64] starting at channel 64*h.
-struct OutRows {
-  rsrc_t out, gate;
-  unsigned ld4, ldg4;
-  bool half, gate_half;
-};
-
-__device__ __forceinline__ OutRows out_rows(const AttnParams& p, int g, int h) {
-  const int T = p.tokens;
-  const long row = group_row(p, g);
-  OutRows o;
-  o.half = p.out_half != 0;
-  const unsigned esize = o.half ? 2 : 4;
-  o.ld4 = (unsigned)(p.tstep * p.heads * 64 * esize);
-  o.out = make_rsrc(reinterpret_cast<unsigned char*>(p.out) + (row * p.heads + h) * 64 * esize,
-                    (unsigned)(T - 1) * o.ld4 + 64 * esize);
-  o.gate_half = p.in_half != 0;
-  const unsigned gsize = o.gate_half ? 2 : 4;
-  o.ldg4 = (unsigned)(p.tstep * p.ldg * gsize);
-  o.gate = make_rsrc(p.gate ? reinterpret_cast<const unsigned char*>(p.gate) +
-                                  (row * p.ldg + h) * gsize
-                            : reinterpret_cast<const unsigned char*>(p.out),
-                     p.gate ? (unsigned)(T - 1) * o.ldg4 + gsize : 0);
-  return o;
 }
 
 // 1/l and sigmoid(gate) scaling and store of one lane's 16 channels (grp*4 + 16*db) of query t.
@@ -635,6 +596,7 @@ static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
     hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED, XH>), dim3(problems),
                        dim3(256), 0, stream, p, problems);
   } else {
+    if constexpr (ALIGNED) return launch_attention_long(p, GATED, ROPE, stream);
     const int qblocks = (T + kTimeQueries - 1) / kTimeQueries;
     const int total = p.groups * p.heads * qblocks;
     hipLaunchKernelGGL((attention_time_kernel<GATED, ROPE, ALIGNED, XH>), dim3(total),
