@@ -144,8 +144,8 @@ static size_t region_packed(const ancha_hip_block* b, size_t rows) {
 // no transposed copy. Every stage but attention and the rotary epilogue is row-wise, so only
 // those two see the layout. out may be x (x is last read before out is first written).
 // xh_in: the workspace already holds fp16(unit_norm(x)) (the previous block's xh_out).
-// xh_out: the output norm also writes fp16(unit_norm(out)) there for the next block (only with
-// an output norm, dim <= 512 and a next block of the same layout; see block_chainable).
+// xh_out: also write fp16(unit_norm(out)) there for the next block (dim <= 512 and a next block
+// of the same shape; see block_chainable).
 static int block_forward(const ancha_hip_block* b, const float* x, size_t groups, size_t tokens,
                          size_t split, const float* rope, void* workspace,
                          size_t workspace_bytes, float* out, hipStream_t stream,
@@ -244,7 +244,7 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
     tp.b2 = b->ff_out_b;
     tp.out_scale = b->out_scale;
     tp.out = out;
-    tp.xh = b->out_scale && xh_out ? xh : nullptr;
+    tp.xh = xh_out ? xh : nullptr;
     tp.rows = static_cast<int>(rows);
     tp.dim = static_cast<int>(dim);
     tp.inner = static_cast<int>(inner);
@@ -266,10 +266,10 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
   rc = gemm(hidden, true, rows, b->hidden, b->ff_out_w, dim, b->ff_out_b, false, nullptr, 0, 1, 0,
             x1, out, false, false, stream);
   if (rc) return rc;
-  if (b->out_scale && xh_out) {
-    // out = unit_norm(out) * scale in place, and the next block's fp16 operand in one pass.
+  if (xh_out) {
+    // [out = unit_norm(out) * scale in place, and] the next block's fp16 operand in one pass.
     e = ancha::launch_norm_half(out, static_cast<int>(rows), static_cast<int>(dim), b->out_scale,
-                                out, xh, stream);
+                                b->out_scale ? out : nullptr, xh, stream);
     if (e != hipSuccess) return ancha::hip_fail(e, "ancha_hip_block_forward");
   } else if (b->out_scale) {
     rc = ancha_hip_unit_norm(out, rows, dim, dim, b->out_scale, out, stream);
@@ -280,7 +280,7 @@ static int block_forward(const ancha_hip_block* b, const float* x, size_t groups
 namespace ancha {
 
 bool block_chainable(const ancha_hip_block* a, const ancha_hip_block* b) {
-  return a && b && a->out_scale && a->dim <= 512 && a->dim == b->dim && a->inner == b->inner &&
+  return a && b && a->dim <= 512 && a->dim == b->dim && a->inner == b->inner &&
          a->columns == b->columns && a->hidden == b->hidden;
 }
 

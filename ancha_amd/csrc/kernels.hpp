@@ -163,7 +163,7 @@ hipError_t launch_qkv(const QkvParams& p, hipStream_t stream);
 // from another product's accumulators (tail.hip): B k-slot 8h + t holds feature kPerm16[8h + t].
 constexpr int kPerm16[16] = {0, 1, 2, 3, 8, 9, 10, 11, 4, 5, 6, 7, 12, 13, 14, 15};
 
-// Axis pair of two blocks (block.hip) whose output norms hand the next block its fp16 operand:
+// Axis pair of two blocks (block.hip) where each block hands the next its fp16 operand:
 // xh_in, the workspace holds fp16(unit_norm(x)) from the previous pair; xh_out, the band block
 // leaves fp16(unit_norm(out)) there for the next pair (which must satisfy block_chainable with
 // it). Between the two blocks of the pair the same hand-over happens when they allow it.

@@ -236,7 +236,7 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
   // Axis loop (network.rs:333-339): x [nch][bands][frames][dim] is the time layout with batch
   // nch.
   const size_t block_bytes = l.total - l.inner;
-  // Each block's output norm also writes the next block's fp16 operand where the blocks allow.
+  // Each block also writes the next block's fp16 operand where the blocks allow.
   bool xh_in = false;
   for (size_t i = 0; i < m->depth; i++) {
     if (cancel_requested(cancelled)) return cancelled_rc();

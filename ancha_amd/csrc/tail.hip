@@ -4,7 +4,8 @@
 //   x1 = x + attended . W_out                          out projection + residual
 //   h  = fp16(GELU(fp16(unit_norm(x1)) . W1' + b1))    FF in (sqrt(dim)*gamma folded into W1')
 //   y  = x1 + h . W2 + b2                              FF out + bias + residual
-//   [y = unit_norm(y) * scale; xh = fp16(unit_norm(y))]   Mel output norm, next block's operand
+//   [y = unit_norm(y) * scale]                          output norm (Mel-RoFormer blocks)
+//   [xh = fp16(unit_norm(y))]                           the next block's operand
 // The rounding points are those of the unfused path (block.hip): fp16 normalised operand, fp16
 // hidden activation, fp32 accumulation and fp32 residual stream.
 //
@@ -314,31 +315,33 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
             acc[i][j][4 * q + 3] = acc[i][j][4 * q + 3] * inv * sc.w;
           }
       }
-      if (p.xh) {
+    }
+    if (p.xh) {
+      // The next block's fp16 operand, fp16(unit_norm(y)) (y after the output norm, if any).
+      float part[2], tot[2];
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          float s = 0.f;
+      for (int j = 0; j < 2; j++) {
+        float s = 0.f;
 #pragma unroll
-          for (int i = 0; i < NI; i++)
+        for (int i = 0; i < NI; i++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) s += acc[i][j][r] * acc[i][j][r];
-          part[j] = s + __shfl_xor(s, 32);
-        }
-        row_totals<2>(red, part, tot, fq, rh, lane);
+          for (int r = 0; r < 16; r++) s += acc[i][j][r] * acc[i][j][r];
+        part[j] = s + __shfl_xor(s, 32);
+      }
+      row_totals<2>(red, part, tot, fq, rh, lane);
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          const float inv = 1.0f / fmaxf(sqrtf(tot[j]), 1e-12f);
+      for (int j = 0; j < 2; j++) {
+        const float inv = 1.0f / fmaxf(sqrtf(tot[j]), 1e-12f);
 #pragma unroll
-          for (int i = 0; i < NI; i++)
+        for (int i = 0; i < NI; i++)
 #pragma unroll
-            for (int q = 0; q < 4; q++) {
-              const u32x2 h = {pack_h2(acc[i][j][4 * q] * inv, acc[i][j][4 * q + 1] * inv),
-                               pack_h2(acc[i][j][4 * q + 2] * inv, acc[i][j][4 * q + 3] * inv)};
-              __builtin_amdgcn_raw_buffer_store_b64(
-                  h, xhr, ((unsigned)(32 * (2 * rh + j) + col) * DIM + 4 * half) * 2,
-                  (unsigned)(32 * (fq * NI + i) + 8 * q) * 2, 0);
-            }
-        }
+          for (int q = 0; q < 4; q++) {
+            const u32x2 h = {pack_h2(acc[i][j][4 * q] * inv, acc[i][j][4 * q + 1] * inv),
+                             pack_h2(acc[i][j][4 * q + 2] * inv, acc[i][j][4 * q + 3] * inv)};
+            __builtin_amdgcn_raw_buffer_store_b64(
+                h, xhr, ((unsigned)(32 * (2 * rh + j) + col) * DIM + 4 * half) * 2,
+                (unsigned)(32 * (fq * NI + i) + 8 * q) * 2, 0);
+          }
       }
     }
 #pragma unroll
