@@ -20,6 +20,9 @@ from . import _native
 from ._tensors import require
 from .plan import AttentionPlan, backend_plan, require_gpu_kernels, run_settings
 
+# Raised by a forward or separation whose CancelFlag was set (C ABI code 3).
+Cancelled = _native.Cancelled
+
 N_FFT = 2048
 BINS = N_FFT // 2 + 1
 CONFIGS = os.path.join(os.path.dirname(os.path.abspath(__file__)), "configs")
