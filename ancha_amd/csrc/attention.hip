@@ -55,31 +55,35 @@ __device__ __forceinline__ unsigned v_pair(u32x2 a, u32x2 b, int j) {
 }
 
 // 1/l and sigmoid(gate) scaling and store of one lane's 16 channels (grp*4 + 16*db) of query t.
-template <bool GATED, bool ALIGNED>
+// HALF: 1 = fp16 gate and output, 0 = fp32 gate and output, -1 = as o.gate_half / o.half say
+// (a branch the compiler's wait counting cannot see through).
+template <bool GATED, bool ALIGNED, int CP = 0, int HALF = -1>
 __device__ __forceinline__ void store_output(const OutRows& o, const f32x4 (&acc)[4], float l,
                                              int t, int grp) {
   float scale = 1.0f / l;
+  const bool gate_half = HALF < 0 ? o.gate_half : HALF > 0;
+  const bool out_half = HALF < 0 ? o.half : HALF > 0;
   if constexpr (GATED) {
     const float gl =
-        o.gate_half ? (float)__builtin_bit_cast(
+        gate_half ? (float)__builtin_bit_cast(
                           _Float16, __builtin_amdgcn_raw_buffer_load_b16(o.gate, (unsigned)t * o.ldg4, 0, 0))
                     : bload1(o.gate, (unsigned)t * o.ldg4);
     scale = scale / (1.0f + expf(-gl));
   }
-  if (o.half) {
+  if (out_half) {
     const unsigned base = (unsigned)t * o.ld4 + grp * 8;
 #pragma unroll
     for (int db = 0; db < 4; db++) {
       const u32x2 h = {pack_h2(acc[db][0] * scale, acc[db][1] * scale),
                        pack_h2(acc[db][2] * scale, acc[db][3] * scale)};
-      __builtin_amdgcn_raw_buffer_store_b64(h, o.out, base + db * 32, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(h, o.out, base + db * 32, 0, CP);
     }
     return;
   }
   const unsigned base = (unsigned)t * o.ld4 + grp * 16;
 #pragma unroll
   for (int db = 0; db < 4; db++)
-    bstore4<ALIGNED>(o.out, base + db * 64,
+    bstore4<ALIGNED, CP>(o.out, base + db * 64,
                      make_float4(acc[db][0] * scale, acc[db][1] * scale, acc[db][2] * scale,
                                  acc[db][3] * scale));
 }
@@ -438,163 +442,267 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
 }
 
 // ------------------------------------------------------------------------------------------
-// Short sequences (T <= 64): one workgroup (4 waves) per (group, head) problem. The whole
-// workgroup stages q, k (rotated, fp16) and v^T (fp16) through LDS with coalesced 16-byte row
+// Short sequences (T <= 64): 4-wave workgroups on (group, head) problems. Per problem the whole
+// workgroup stages q, k (rotated, fp16) and v^T (fp16) through LDS from coalesced 16-byte row
 // loads, all issued at once; then wave w computes queries 16w .. 16w+15 against all keys with
-// an exact softmax. Small workgroups with few registers keep many problems' loads in flight
-// per CU, which is what this HBM-bound shape needs.
+// an exact softmax. The shape is HBM-bound: q / k / v and the output are streamed
+// (non-temporal), each byte being touched once. Two ways to keep loads in flight:
+//
+//  * fp32 input (the op boundary): persistent workgroups, as many as the CUs hold, each walking
+//    problems b, b + grid, ... in two alternating register sets: once a problem is staged, the
+//    next one's loads are issued and stay in flight through the current compute and its
+//    stores. A thread stages the same rows and channels of every problem, so its rotary table
+//    values are loaded once, into registers, for the whole walk.
+//  * fp16 input (the network's packed projection): one problem per workgroup; with half the
+//    bytes and registers per problem, six workgroups per CU keep enough loads in flight.
+//    Workgroups are dealt to the eight XCDs round-robin (workgroup b to XCD b % 8), each with
+//    its own L2, and the heads of one group are pieces of the same token rows, so the order
+//    gives one XCD all heads of a group on consecutive workgroups: with chunks of 8 * heads
+//    workgroups, workgroup b (chunk c = b / (8 * heads), r = b % (8 * heads)) takes group
+//    8c + r % 8, head r / 8; groups past the last whole chunk of eight keep the plain order.
 // ------------------------------------------------------------------------------------------
+__device__ __forceinline__ void band_problem(int b, int groups, int heads, int& g, int& h) {
+  const int chunk = kXcds * heads;
+  if (b < (groups / kXcds) * chunk) {
+    const int c = b / chunk, r = b - c * chunk;
+    g = c * kXcds + r % kXcds;
+    h = r / kXcds;
+  } else {
+    g = b / heads;
+    h = b - g * heads;
+  }
+}
+
+// One problem's raw rows in the staging roles (below) of one thread.
+template <bool XH>
+struct BandRaw;
+template <>
+struct BandRaw<false> {
+  float4 q[4], k[4], v[4];
+};
+template <>
+struct BandRaw<true> {
+  u32x4 q[2], k[2];
+  u32x2 v[4];
+};
+
 template <bool GATED, bool ROPE, bool ALIGNED, bool XH>
 __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int problems) {
+  static_assert(!(XH && ROPE), "fp16 input arrives rotated");
+  constexpr bool kWalk = !XH;
   __shared__ __attribute__((aligned(16))) unsigned char lds_q[64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_k[64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_v[64 * 128];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int prob = blockIdx.x;
-  const int h = prob % p.heads, g = prob / p.heads;
   const int T = p.tokens;
-  const long row0 = group_row(p, g), ts = p.tstep;
+  const long ts = p.tstep;
   constexpr unsigned kEsz = XH ? 2 : 4, kRowBytes = 64 * kEsz;
   const unsigned ldq4 = (unsigned)(ts * p.ldq * kEsz), ldk4 = (unsigned)(ts * p.ldk * kEsz),
                  ldv4 = (unsigned)(ts * p.ldv * kEsz);
-  auto rows_of = [&](const float* base, long ld, unsigned ld4) {
-    return make_rsrc(reinterpret_cast<const unsigned char*>(base) + (row0 * ld + h * 64) * kEsz,
-                     (unsigned)(T - 1) * ld4 + kRowBytes);
-  };
-  const rsrc_t qr = rows_of(p.q, p.ldq, ldq4);
-  const rsrc_t kr = rows_of(p.k, p.ldk, ldk4);
-  const rsrc_t vr = rows_of(p.v, p.ldv, ldv4);
 
-  // Staging: q / k rows srow + 16*it at channels 4*sc; v key pairs (2*(srow + 16*it), +1),
-  // it < 2. Rows at or past T read as 0.
+  // Staging roles: q / k rows srow + 16*it at channels 4*sc; v key pairs (2*(srow + 16*it),
+  // +1), it < 2. fp16 input: q / k rows (tid >> 3) + 32*it as 16-byte chunks tid & 7, v key
+  // pairs at 8-byte channel groups sc. Rows at or past T read as 0.
   const int srow = tid >> 4, sc = tid & 15;
-  if constexpr (XH) {
-    // fp16 rows (q already scaled): q / k rows (tid >> 3) + 32*it as 16-byte chunks tid & 7,
-    // v key pairs at 8-byte channel groups sc.
-    u32x4 hq[2], hk[2];
-    u32x2 hv[4];
+  // This thread's rotary table values (query cos / sin, key cos / sin of its four rows).
+  float4 tab[4][4];
+  if constexpr (ROPE) {
+    const rsrc_t tr = make_rsrc(p.rope, (unsigned)T * 1024);
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const unsigned r = (unsigned)((tid >> 3) + 32 * it);
-      hq[it] = __builtin_amdgcn_raw_buffer_load_b128(qr, r * ldq4 + (tid & 7) * 16, 0, 0);
-      hk[it] = __builtin_amdgcn_raw_buffer_load_b128(kr, r * ldk4 + (tid & 7) * 16, 0, 0);
-    }
+    for (int it = 0; it < 4; it++)
 #pragma unroll
-    for (int it = 0; it < 2; it++)
+      for (int t = 0; t < 4; t++)
+        tab[it][t] = bload4<ALIGNED>(tr, (unsigned)(t * T + srow + 16 * it) * 256 + sc * 16);
+  }
+  auto load = [&](int g, int h, BandRaw<XH>& r) {
+    const long row0 = group_row(p, g);
+    auto rows_of = [&](const float* base, long ld, unsigned ld4) {
+      return make_rsrc(reinterpret_cast<const unsigned char*>(base) + (row0 * ld + h * 64) * kEsz,
+                       (unsigned)(T - 1) * ld4 + kRowBytes);
+    };
+    const rsrc_t qr = rows_of(p.q, p.ldq, ldq4);
+    const rsrc_t kr = rows_of(p.k, p.ldk, ldk4);
+    const rsrc_t vr = rows_of(p.v, p.ldv, ldv4);
+    if constexpr (XH) {
 #pragma unroll
-      for (int r = 0; r < 2; r++)
-        hv[it * 2 + r] = __builtin_amdgcn_raw_buffer_load_b64(
-            vr, (unsigned)(2 * (srow + 16 * it) + r) * ldv4 + sc * 8, 0, 0);
+      for (int it = 0; it < 2; it++) {
+        const unsigned rr = (unsigned)((tid >> 3) + 32 * it);
+        r.q[it] = __builtin_amdgcn_raw_buffer_load_b128(qr, rr * ldq4 + (tid & 7) * 16, 0, kStream);
+        r.k[it] = __builtin_amdgcn_raw_buffer_load_b128(kr, rr * ldk4 + (tid & 7) * 16, 0, kStream);
+      }
 #pragma unroll
-    for (int it = 0; it < 2; it++) {
-      const int off = k_offset((tid >> 3) + 32 * it, tid & 7);
-      *reinterpret_cast<u32x4*>(lds_q + off) = hq[it];
-      *reinterpret_cast<u32x4*>(lds_k + off) = hk[it];
-    }
+      for (int it = 0; it < 2; it++)
 #pragma unroll
-    for (int it = 0; it < 2; it++)
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
-            v_pair(hv[it * 2], hv[it * 2 + 1], j);
-  } else {
-    float4 xq[4], xk[4], xv[4];
-#pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const unsigned r = (unsigned)(srow + 16 * it);
-      xq[it] = bload4<ALIGNED>(qr, r * ldq4 + sc * 16);
-      xk[it] = bload4<ALIGNED>(kr, r * ldk4 + sc * 16);
-    }
-#pragma unroll
-    for (int it = 0; it < 2; it++)
-#pragma unroll
-      for (int r = 0; r < 2; r++)
-        xv[it * 2 + r] = bload4<ALIGNED>(vr, (unsigned)(2 * (srow + 16 * it) + r) * ldv4 + sc * 16);
-    if constexpr (ROPE) {
-      const rsrc_t tr = make_rsrc(p.rope, (unsigned)T * 1024);
+        for (int j = 0; j < 2; j++)
+          r.v[it * 2 + j] = __builtin_amdgcn_raw_buffer_load_b64(
+              vr, (unsigned)(2 * (srow + 16 * it) + j) * ldv4 + sc * 8, 0, kStream);
+    } else {
 #pragma unroll
       for (int it = 0; it < 4; it++) {
-        const unsigned o = (unsigned)(srow + 16 * it) * 256 + sc * 16, plane = (unsigned)T * 256;
-        xq[it] = rotate4(xq[it], bload4<ALIGNED>(tr, o), bload4<ALIGNED>(tr, o + plane));
-        xk[it] = rotate4(xk[it], bload4<ALIGNED>(tr, o + 2 * plane),
-                         bload4<ALIGNED>(tr, o + 3 * plane));
+        const unsigned rr = (unsigned)(srow + 16 * it);
+        r.q[it] = bload4<ALIGNED, kStream>(qr, rr * ldq4 + sc * 16);
+        r.k[it] = bload4<ALIGNED, kStream>(kr, rr * ldk4 + sc * 16);
       }
+#pragma unroll
+      for (int it = 0; it < 2; it++)
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          r.v[it * 2 + j] =
+              bload4<ALIGNED, kStream>(vr, (unsigned)(2 * (srow + 16 * it) + j) * ldv4 + sc * 16);
     }
+  };
+  auto stage = [&](const BandRaw<XH>& r) {
+    if constexpr (XH) {
 #pragma unroll
-    for (int it = 0; it < 4; it++) {
-      const int r = srow + 16 * it;
-      const float4 q = scale4(xq[it], kLog2e), k = xk[it];
-      const int off = k_offset(r, sc >> 1) + ((sc & 1) << 3);
-      *reinterpret_cast<u32x2*>(lds_q + off) = u32x2{pack_h2(q.x, q.y), pack_h2(q.z, q.w)};
-      *reinterpret_cast<u32x2*>(lds_k + off) = u32x2{pack_h2(k.x, k.y), pack_h2(k.z, k.w)};
+      for (int it = 0; it < 2; it++) {
+        const int off = k_offset((tid >> 3) + 32 * it, tid & 7);
+        *reinterpret_cast<u32x4*>(lds_q + off) = r.q[it];
+        *reinterpret_cast<u32x4*>(lds_k + off) = r.k[it];
+      }
+#pragma unroll
+      for (int it = 0; it < 2; it++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+              v_pair(r.v[it * 2], r.v[it * 2 + 1], j);
+    } else {
+#pragma unroll
+      for (int it = 0; it < 4; it++) {
+        const int rr = srow + 16 * it;
+        float4 q = r.q[it], k = r.k[it];
+        if constexpr (ROPE) {
+          q = rotate4(q, tab[it][0], tab[it][1]);
+          k = rotate4(k, tab[it][2], tab[it][3]);
+        }
+        q = scale4(q, kLog2e);
+        const int off = k_offset(rr, sc >> 1) + ((sc & 1) << 3);
+        *reinterpret_cast<u32x2*>(lds_q + off) = u32x2{pack_h2(q.x, q.y), pack_h2(q.z, q.w)};
+        *reinterpret_cast<u32x2*>(lds_k + off) = u32x2{pack_h2(k.x, k.y), pack_h2(k.z, k.w)};
+      }
+#pragma unroll
+      for (int it = 0; it < 2; it++)
+#pragma unroll
+        for (int j = 0; j < 4; j++)
+          *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+              pack_h2(comp(r.v[it * 2], j), comp(r.v[it * 2 + 1], j));
     }
-#pragma unroll
-    for (int it = 0; it < 2; it++)
-#pragma unroll
-      for (int j = 0; j < 4; j++)
-        *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
-            pack_h2(comp(xv[it * 2], j), comp(xv[it * 2 + 1], j));
-  }
-  __syncthreads();
+  };
 
   const int q0 = wave * 16;
-  if (q0 >= T) return;
   const int kq_base[2] = {k_offset(col, grp), k_offset(col, 4 + grp)};
   const int vsw = (col ^ (col >> 2)) & 7;
   const int v_base[2][2] = {{col * 128 + ((grp ^ vsw) << 4), col * 128 + ((grp ^ vsw ^ 4) << 4)},
                             {col * 128 + (((4 + grp) ^ vsw) << 4),
                              col * 128 + (((4 + grp) ^ vsw ^ 4) << 4)}};
-  const u32x4 qf[2] = {*reinterpret_cast<const u32x4*>(lds_q + kq_base[0] + wave * 2048),
-                       *reinterpret_cast<const u32x4*>(lds_q + kq_base[1] + wave * 2048)};
-  f32x4 s[4];
+  auto compute = [&](int g, int h) {
+    const u32x4 qf[2] = {*reinterpret_cast<const u32x4*>(lds_q + kq_base[0] + wave * 2048),
+                         *reinterpret_cast<const u32x4*>(lds_q + kq_base[1] + wave * 2048)};
+    f32x4 s[4];
 #pragma unroll
-  for (int kb = 0; kb < 4; kb++) {
-    s[kb] = zero4();
+    for (int kb = 0; kb < 4; kb++) {
+      s[kb] = zero4();
 #pragma unroll
-    for (int ds = 0; ds < 2; ds++)
-      s[kb] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_k + kq_base[ds] + kb * 2048),
-                           qf[ds], s[kb]);
-  }
-  if (T < 64) {
+      for (int ds = 0; ds < 2; ds++)
+        s[kb] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_k + kq_base[ds] + kb * 2048),
+                             qf[ds], s[kb]);
+    }
+    if (T < 64) {
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+          if (kb * 16 + grp * 4 + r >= T) s[kb][r] = kMasked;
+    }
+    float mx = kMasked;
 #pragma unroll
     for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-      for (int r = 0; r < 4; r++)
-        if (kb * 16 + grp * 4 + r >= T) s[kb][r] = kMasked;
+      for (int r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][r]);
+    mx = max_over_rows(mx);
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) s[kb][r] = fast_exp2(s[kb][r] - mx);
+    const u32x4 pf[2] = {p_fragment(s[0], s[1]), p_fragment(s[2], s[3])};
+    const u32x4 ones = {kOnesH2, kOnesH2, kOnesH2, kOnesH2};
+    f32x4 o[4] = {zero4(), zero4(), zero4(), zero4()}, lsum = zero4();
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+      for (int db = 0; db < 4; db++)
+        o[db] = mfma16x16x32(
+            *reinterpret_cast<const u32x4*>(lds_v + v_base[ks][db & 1] + db * 2048), pf[ks], o[db]);
+      lsum = mfma16x16x32(ones, pf[ks], lsum);
+    }
+    // fp16 input stores fp16 (fixed at compile time: no branch between the loads and the
+    // waits, 1.5 % off the layer). The fp32 walk keeps the run-time form: with the branch
+    // removed the compiler's wait placement changes and the walk measured 5 % slower.
+    store_output<GATED, ALIGNED, kStream, XH ? 1 : -1>(out_rows(p, g, h), o, lsum[0], q0 + col,
+                                                       grp);
+  };
+
+  if constexpr (kWalk) {
+    // Workgroup-uniform: every wave runs every step and reaches both barriers. The next loads
+    // go out after the staging barrier and ahead of this problem's stores, so the wait before
+    // the next staging leaves those stores outstanding. Past the end they reload the last
+    // problem (unused), and a wave whose 16 queries all lie at or past T (T <= 48) computes
+    // anyway (its q rows are zero; rows at or past T lie outside the output's buffer range, so
+    // their stores are dropped): no branch around the loads and stores keeps the wait counts
+    // fixed.
+    auto step = [&](int prob, const BandRaw<XH>& cur, BandRaw<XH>& nxt) {
+      stage(cur);
+      __syncthreads();
+      const int next = min(prob + (int)gridDim.x, problems - 1);
+      load(next / p.heads, next % p.heads, nxt);
+      compute(prob / p.heads, prob % p.heads);
+      __syncthreads();  // the next step restages LDS
+    };
+    // The first step is peeled so the loop is entered with the same loads and stores
+    // outstanding as each turn ends with (else the wait counts at the loop head are merged down
+    // to a full drain).
+    BandRaw<XH> a, b;
+    int prob = blockIdx.x;
+    load(prob / p.heads, prob % p.heads, a);
+    step(prob, a, b);
+    while (true) {
+      prob += gridDim.x;
+      if (prob >= problems) break;
+      step(prob, b, a);
+      prob += gridDim.x;
+      if (prob >= problems) break;
+      step(prob, a, b);
+    }
+  } else {
+    int g, h;
+    band_problem(blockIdx.x, p.groups, p.heads, g, h);
+    BandRaw<XH> r;
+    load(g, h, r);
+    stage(r);
+    __syncthreads();
+    if (q0 < T) compute(g, h);
   }
-  float mx = kMasked;
-#pragma unroll
-  for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) mx = fmaxf(mx, s[kb][r]);
-  mx = max_over_rows(mx);
-#pragma unroll
-  for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-    for (int r = 0; r < 4; r++) s[kb][r] = fast_exp2(s[kb][r] - mx);
-  const u32x4 pf[2] = {p_fragment(s[0], s[1]), p_fragment(s[2], s[3])};
-  const u32x4 ones = {kOnesH2, kOnesH2, kOnesH2, kOnesH2};
-  f32x4 o[4] = {zero4(), zero4(), zero4(), zero4()}, lsum = zero4();
-#pragma unroll
-  for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-    for (int db = 0; db < 4; db++)
-      o[db] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_v + v_base[ks][db & 1] + db * 2048),
-                           pf[ks], o[db]);
-    lsum = mfma16x16x32(ones, pf[ks], lsum);
-  }
-  store_output<GATED, ALIGNED>(out_rows(p, g, h), o, lsum[0], q0 + col, grp);
 }
 
 template <bool GATED, bool ROPE, bool ALIGNED, bool XH = false>
 static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
   const int T = p.tokens;
   if (T <= 64) {
+    auto kernel = attention_band_kernel<GATED, ROPE, ALIGNED, XH>;
     const int problems = p.groups * p.heads;
-    hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED, XH>), dim3(problems),
-                       dim3(256), 0, stream, p, problems);
+    int grid = problems;
+    if constexpr (!XH) {
+      // The walk: as many workgroups as the CUs hold at once.
+      static int per_cu = 0;
+      if (per_cu <= 0 &&
+          (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess ||
+           per_cu <= 0))
+        per_cu = 2;
+      const long cap = (long)per_cu * device_cus();
+      if (cap < problems) grid = (int)cap;
+    }
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, stream, p, problems);
   } else {
     if constexpr (ALIGNED) return launch_attention_long(p, GATED, ROPE, stream);
     const int qblocks = (T + kTimeQueries - 1) / kTimeQueries;
@@ -623,6 +731,7 @@ hipError_t launch_attention(const AttnParams& params, bool aligned, hipStream_t 
     p.tstep = 1;
   }
   const bool gated = p.gate != nullptr, rope = p.rope != nullptr;
+  if ((p.in_half != 0) != (p.out_half != 0)) return hipErrorInvalidValue;
   if (p.in_half) {
     // The block's packed fp16 projection only.
     if (!gated || rope || !aligned) return hipErrorInvalidValue;

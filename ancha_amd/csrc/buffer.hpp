@@ -21,27 +21,31 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, unsigned bytes) {
                                            0x00020000);
 }
 
-template <bool ALIGNED>
+// Cache policy of a buffer access (gfx950): 0 = default; kStream = non-temporal, for data that
+// is read or written exactly once (streamed past the caches' reuse).
+constexpr int kStream = 2;
+
+template <bool ALIGNED, int CP = 0>
 __device__ __forceinline__ float4 bload4(rsrc_t r, unsigned off) {
   if constexpr (ALIGNED) {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CP));
   } else {
-    return make_float4(__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0)),
-                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, 0)),
-                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 8, 0, 0)),
-                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 12, 0, 0)));
+    return make_float4(__builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CP)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 4, 0, CP)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 8, 0, CP)),
+                       __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off + 12, 0, CP)));
   }
 }
 
-template <bool ALIGNED>
+template <bool ALIGNED, int CP = 0>
 __device__ __forceinline__ void bstore4(rsrc_t r, unsigned off, float4 v) {
   if constexpr (ALIGNED) {
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, CP);
   } else {
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.x), r, off, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.y), r, off + 4, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.z), r, off + 8, 0, 0);
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.w), r, off + 12, 0, 0);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.x), r, off, 0, CP);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.y), r, off + 4, 0, CP);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.z), r, off + 8, 0, CP);
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v.w), r, off + 12, 0, CP);
   }
 }
 

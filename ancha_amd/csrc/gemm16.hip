@@ -344,7 +344,8 @@ void launch(const Gemm16Params& p, int grid, int col_tiles, int tiles, hipStream
   launch_epi<XH, OH, NORM, kEpiRuntime>(p, grid, col_tiles, tiles, stream);
 }
 
-// Compute units of the current device (cached per device).
+}  // namespace
+
 int device_cus() {
   static int cached[64] = {0};
   int dev = 0;
@@ -358,8 +359,6 @@ int device_cus() {
   }
   return cached[dev];
 }
-
-}  // namespace
 
 hipError_t launch_gemm16(const Gemm16Params& p, hipStream_t stream) {
   const int row_tiles = (p.n + kBM - 1) / kBM, col_tiles = p.m / kBN;

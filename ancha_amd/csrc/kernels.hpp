@@ -23,13 +23,16 @@ struct AttnParams {
   float* out;         // [groups, tokens, heads, 64] contiguous (fp16 values if out_half)
   long ldq, ldk, ldv, ldg;
   int groups, tokens, heads;
-  int out_half;       // store the output as fp16 (the block's internal activation)
+  int out_half;       // store the output as fp16 (the block's internal activation); set with in_half
   // q / k / v / gate are fp16 (ld* in fp16 elements) and q already carries log2(e) with the
   // softmax scale: the block's packed projection. Gated, rope-free, 16-byte aligned calls only.
   int in_half;
   int gsplit;
   long gouter, gstep, tstep;
 };
+
+// Compute units of the current device (looked up once per device; 256 if the query fails).
+int device_cus();
 
 // `aligned`: every float4 access is 16-byte aligned (base pointers and row strides).
 hipError_t launch_attention(const AttnParams& p, bool aligned, hipStream_t stream);

@@ -183,11 +183,7 @@ hipError_t launch_qkv(const QkvParams& p, hipStream_t stream) {
   if (!qkv_supported(p.dim, p.cols) || (p.rope && (p.tokens <= 0 || p.token_div <= 0)))
     return hipErrorInvalidValue;
   if (p.rows <= 0) return hipSuccess;
-  int cus = 0, dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus <= 0)
-    cus = 256;
+  const int cus = device_cus();
   const int blocks = (p.rows + kRows - 1) / kRows;
   const int grid = blocks < cus ? blocks : cus;
   switch (p.dim) {

@@ -377,11 +377,7 @@ bool block_tail_supported(int dim, int inner, int hidden) {
 hipError_t launch_block_tail(const TailParams& p, hipStream_t stream) {
   if (!block_tail_supported(p.dim, p.inner, p.hidden)) return hipErrorInvalidValue;
   if (p.rows <= 0) return hipSuccess;
-  int cus = 0, dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus <= 0)
-    cus = 256;
+  const int cus = device_cus();
   const int blocks = (p.rows + kRows - 1) / kRows;
   const int grid = blocks < 2 * cus ? blocks : 2 * cus;  // two workgroups per CU
   const int ni = p.dim / 128;

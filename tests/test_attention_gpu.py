@@ -148,16 +148,50 @@ def test_time_axis_full_size(gpu):
     assert torch.equal(out, again), "kernel must be deterministic"
 
 
+def torch_attention(q, k, v, table):
+    """fp32 torch restatement used only where the oracle would be too slow: every group at the
+    production size. q, k, v [G, T, H, 64]; table [4, T, 64] (q cos, q sin, k cos, k sin)."""
+    def rotate(x, c, s):
+        sw = torch.stack([x[..., 1::2], x[..., 0::2]], dim=-1).reshape(x.shape)
+        return x * c[None, :, None, :] + sw * s[None, :, None, :]
+
+    g, t, h, d = q.shape
+    per_head = lambda x: x.permute(0, 2, 1, 3).reshape(g * h, t, d).contiguous()
+    qr, kr, vh = per_head(rotate(q, table[0], table[1])), per_head(rotate(k, table[2], table[3])), \
+        per_head(v)
+    p = torch.softmax(torch.matmul(qr, kr.transpose(1, 2).contiguous()), dim=-1)
+    return torch.matmul(p, vh).reshape(g, h, t, d).permute(0, 2, 1, 3)
+
+
 def test_band_axis_full_size(gpu):
-    """The band-axis op at its production size [1602, 60, 8, 64]."""
+    """The band-axis op at its production size [1602, 60, 8, 64]: sampled groups against the
+    oracle (including the last two, outside the whole chunks of eight groups of the kernel's
+    XCD-grouped problem order) and every group against an fp32 torch restatement."""
     q, k, v = seeded(W.BAND_SHAPE, gpu)
     table = W.axis_rope_packed(W.rope_freqs(), W.BAND_SHAPE[1])
-    out = fused.attention(q, k, v, rope=dev(table, gpu))
+    tq = dev(table, gpu)
+    out = fused.attention(q, k, v, rope=tq)
     torch.cuda.synchronize()
     assert torch.isfinite(out).all()
-    groups = [0, 1, 800, 1601]
+    groups = [0, 1, 7, 8, 800, 1599, 1600, 1601]
     expected = oracle_slice(q, k, v, table, groups)
     check("band full-size", out[groups].cpu().numpy(), expected)
+    ref = torch_attention(q, k, v, tq)
+    err, scale = (out - ref).abs().max().item(), ref.abs().max().item()
+    report("band full-size, every group vs fp32 torch", err)
+    assert err < TOL and err <= REL * scale, (err, scale)
+
+
+@pytest.mark.parametrize("groups,tokens,heads", [(19, 60, 3), (17, 33, 8), (8, 64, 5)])
+def test_band_problem_order_covers_every_problem(gpu, groups, tokens, heads):
+    """Short-sequence problems are taken in an XCD-grouped order (whole chunks of eight groups,
+    then the rest in plain order): every (group, head) must be computed once, for group counts
+    that are not a multiple of eight and head counts other than eight."""
+    q, k, v = seeded((groups, tokens, heads, 64), gpu)
+    table = W.axis_rope_packed(W.rope_freqs(), tokens)
+    got = fused.attention(q, k, v, rope=dev(table, gpu)).cpu().numpy()
+    expected = O.attention_op(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), rope=table)
+    check(f"band order {groups}x{tokens}x{heads}", got, expected)
 
 
 @pytest.mark.parametrize("tokens", [60, 801])
