@@ -3,11 +3,20 @@
 // attention.hip (crates/ancha-models/src/fused/attention.rs:26-227): softmax(q.k^T).v per
 // (group, head), optional interleaved RoPE on load, optional per-head sigmoid gate.
 //
-// One workgroup = 16 waves x 32 queries of one (group, head); each 64-key tile is staged once
-// into LDS as fp16 (K rotated on the way) and read by all 16 waves. The kernel is bound by the
-// VALU work of the softmax (exp2, max, fp16 packing: about as many cycles as the MFMAs), so it
-// is built for overlap: at most 128 VGPRs, which puts four waves on every SIMD, one wave's
-// softmax running beside another's MFMAs.
+// Work unit ("pass") = 512 queries of one (group, head): 16 waves x 32 queries; each 64-key tile
+// is staged once into LDS as fp16 (K rotated on the way) and read by all 16 waves. Workgroups
+// are persistent, one per CU, and walk the passes in rounds; the walk is pipelined so that a
+// pass starts with its inputs already on chip: while a pass runs its K/V tiles, each wave
+// prefetches the next pass's 32 query rows (fp32 inputs: rows plus their rotary table rows, in
+// 4-row chunks landing in LDS by direct buffer loads, rotated and packed to fp16 at the end of
+// the step), and the next pass's first K/V tile loads beside this pass's epilogue. Output rows
+// are stored after the step's loads have landed, so they drain behind the next pass. Within a
+// step the next tile's K / V rows are requested first and its table rows (and the query chunk)
+// after the first 32-key block, so the 16 waves' requests do not all queue at once.
+//
+// The softmax VALU work (exp2, max, fp16 packing) costs about as many cycles as the MFMAs, so
+// the kernel is built for overlap: at most 128 VGPRs, which puts four waves on every SIMD, one
+// wave's softmax running beside another's MFMAs.
 //
 // Per 32-key block a wave computes S^T = K.Q^T (4 MFMAs over head_dim 64) with the accumulator
 // seeded with -m, so the scores come out already shifted by the running maximum; each lane then
@@ -26,6 +35,11 @@ namespace {
 
 constexpr int kWaves = 16;
 constexpr int kQueries = kWaves * 32;
+// Prefetch of the next pass's query rows, one chunk per K/V step: fp32 inputs in 8 chunks of 4
+// rows (each with its cos and sin table rows: 3 x 1 KB per wave), fp16 inputs in 4 chunks of 8
+// rows (1 KB per wave, loaded straight into place).
+template <bool XH>
+constexpr int kChunks = XH ? 4 : 8;
 
 // Byte offset of 16-byte chunk c (0..7) of row r in a tile of 128-byte rows (K: row = key;
 // V^T: row = channel; a wave's queries: row = query). Chunks are XOR-swizzled by (r >> 1) & 7,
@@ -98,53 +112,83 @@ __device__ __forceinline__ u32x4 lds16(const unsigned char* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
 
+// Zero accumulator built in place by asm moves: a value of its own in every pass (the compiler
+// cannot hoist it out of the pass loop and hold it in registers across the walk), and a
+// register C operand, so the MFMA it starts is tied to it (see mfma32_zero).
+__device__ __forceinline__ f32x16 zero16() {
+  f32x2 a[8];
+#pragma unroll
+  for (int i = 0; i < 8; i++) asm volatile("v_mov_b64 %0, 0" : "=v"(a[i]));
+  const f32x4v b[4] = {__builtin_shufflevector(a[0], a[1], 0, 1, 2, 3),
+                       __builtin_shufflevector(a[2], a[3], 0, 1, 2, 3),
+                       __builtin_shufflevector(a[4], a[5], 0, 1, 2, 3),
+                       __builtin_shufflevector(a[6], a[7], 0, 1, 2, 3)};
+  const f32x8 c0 = __builtin_shufflevector(b[0], b[1], 0, 1, 2, 3, 4, 5, 6, 7);
+  const f32x8 c1 = __builtin_shufflevector(b[2], b[3], 0, 1, 2, 3, 4, 5, 6, 7);
+  return __builtin_shufflevector(c0, c1, 0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+}
+
+// LDS-direct buffer load: each lane's 16 bytes at `off` land at dst + 16 * lane.
+__device__ __forceinline__ void load_lds16(rsrc_t r, unsigned char* dst, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
+                                           off, 0, 0, 0);
+}
+
 template <bool GATED, bool ROPE, bool XH>
-__global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnParams p,
-                                                                        int qblocks, int total) {
+__global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnParams p, int qblocks,
+                                                                        int passes) {
   // K tile: row = key (128 bytes of fp16 channels); V^T tile: row = channel (64 keys in
-  // v_position order). Double buffered.
+  // v_position order). Double buffered, the buffer index running on across passes.
   __shared__ __attribute__((aligned(16))) unsigned char lds_k[2][64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_v[2][64 * 128];
-  // Each wave's 32 queries (fp16 rows), staged once.
+  // Each wave's 32 queries of the next pass (fp16 rows), read into registers when it starts.
   __shared__ __attribute__((aligned(16))) unsigned char lds_q[kWaves][32 * 128];
-  const int tid = threadIdx.x, lane = tid & 63;
+  // fp32 inputs: one prefetched chunk per wave (4 query rows, their cos rows, their sin rows).
+  __shared__ __attribute__((aligned(16))) unsigned char lds_raw[XH ? 1 : kWaves][XH ? 16 : 3072];
+  constexpr int kCh = kChunks<XH>;
+  const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5, col = lane & 31;
-  const int logical = xcd_remap(blockIdx.x, total);
-  const int qblk = logical % qblocks, gh = logical / qblocks;
-  const int h = gh % p.heads, g = gh / p.heads;
-  const int T = p.tokens;
-  const long row0 = group_row(p, g), ts = p.tstep;
+  const int grid = gridDim.x;
+  const int lb = xcd_remap(blockIdx.x, grid);
+  const long ts = p.tstep;
   constexpr unsigned kEsz = XH ? 2 : 4, kRowBytes = 64 * kEsz;
-  const unsigned ldq4 = (unsigned)(ts * p.ldq * kEsz), ldk4 = (unsigned)(ts * p.ldk * kEsz),
-                 ldv4 = (unsigned)(ts * p.ldv * kEsz);
-  const unsigned char* kbase =
-      reinterpret_cast<const unsigned char*>(p.k) + (row0 * p.ldk + h * 64) * kEsz;
-  const unsigned char* vbase =
-      reinterpret_cast<const unsigned char*>(p.v) + (row0 * p.ldv + h * 64) * kEsz;
-  const int q0 = qblk * kQueries + wave * 32;
-  const bool active = q0 < T;
+  const int ntiles = (p.tokens + 63) / 64;
+  // Passes run in rounds of `grid`; odd rounds walk backwards, so a workgroup alternates between
+  // the full and the partial query blocks of a (group, head) and both halves of one (group,
+  // head) run side by side on neighbouring workgroups of one XCD (shared K / V in its L2).
+  auto pass_of = [&](int rnd) -> long {
+    return (long)rnd * grid + ((rnd & 1) ? grid - 1 - lb : lb);
+  };
+  // Per-pass opaque copies (set at the top of every pass): the compiler cannot hoist values
+  // derived from them out of the pass loop and hold them in registers across the whole walk.
+  int T = p.tokens, lane = tid & 63, tid_o = tid;
+  unsigned ldq4 = (unsigned)(ts * p.ldq * kEsz), ldk4 = (unsigned)(ts * p.ldk * kEsz),
+           ldv4 = (unsigned)(ts * p.ldv * kEsz);
 
-  // Staging: thread -> key skey of the tile, channels 4 sc .. 4 sc + 3 of K and V (16 threads
-  // read one 256-byte fp32 row). Lanes l and l ^ 16 hold keys 2i and 2i + 1: V^T dwords pair
-  // them, so each lane writes two channels of its key pair (even key: 4 sc, 4 sc + 1; odd key:
-  // 4 sc + 2, 4 sc + 3) after trading halves with its partner.
-  const int skey = tid >> 4, sc = tid & 15;
-  const bool odd = (skey & 1) != 0;
-  const int vch = 4 * sc + 2 * (int)odd, vpos = v_position(skey & ~1);
+  // K / V staging: thread -> key skey of the tile, channels 4 sc .. 4 sc + 3 of K and V (16
+  // threads read one 256-byte fp32 row). Lanes l and l ^ 16 hold keys 2i and 2i + 1: V^T dwords
+  // pair them, so each lane writes two channels of its key pair (even key: 4 sc, 4 sc + 1; odd
+  // key: 4 sc + 2, 4 sc + 3) after trading halves with its partner.
   float4 kx = {}, kc = {}, ks = {}, vx = {};
   u32x2 kh = {}, vh = {};
-  auto load_tile = [&](int key0) {
+  // parts: 0 = K / V and the key table rows, 1 = K / V only, 2 = the table rows only.
+  auto load_tile = [&](const unsigned char* kbase, const unsigned char* vbase, int key0,
+                       int parts) {
+    const int skey = tid_o >> 4, sc = tid_o & 15;
     const unsigned rows = (unsigned)(T - key0);
-    const rsrc_t kr = make_rsrc(kbase + (long)key0 * ldk4, (rows - 1) * ldk4 + kRowBytes);
-    const rsrc_t vr = make_rsrc(vbase + (long)key0 * ldv4, (rows - 1) * ldv4 + kRowBytes);
-    if constexpr (XH) {
-      kh = __builtin_amdgcn_raw_buffer_load_b64(kr, (unsigned)skey * ldk4 + sc * 8, 0, 0);
-      vh = __builtin_amdgcn_raw_buffer_load_b64(vr, (unsigned)skey * ldv4 + sc * 8, 0, 0);
-    } else {
-      kx = bload4<true>(kr, (unsigned)skey * ldk4 + sc * 16);
-      vx = bload4<true>(vr, (unsigned)skey * ldv4 + sc * 16);
-      if constexpr (ROPE) {
+    if (parts != 2) {
+      const rsrc_t kr = make_rsrc(kbase + (long)key0 * ldk4, (rows - 1) * ldk4 + kRowBytes);
+      const rsrc_t vr = make_rsrc(vbase + (long)key0 * ldv4, (rows - 1) * ldv4 + kRowBytes);
+      if constexpr (XH) {
+        kh = __builtin_amdgcn_raw_buffer_load_b64(kr, (unsigned)skey * ldk4 + sc * 8, 0, 0);
+        vh = __builtin_amdgcn_raw_buffer_load_b64(vr, (unsigned)skey * ldv4 + sc * 8, 0, 0);
+      } else {
+        kx = bload4<true>(kr, (unsigned)skey * ldk4 + sc * 16);
+        vx = bload4<true>(vr, (unsigned)skey * ldv4 + sc * 16);
+      }
+    }
+    if constexpr (ROPE && !XH) {
+      if (parts != 1) {
         // Key cos rows (table 2) and sign-folded sin rows (table 3) of this tile.
         const rsrc_t cr = make_rsrc(p.rope + (long)(2 * T + key0) * 64, rows * 256);
         const rsrc_t sr = make_rsrc(p.rope + (long)(3 * T + key0) * 64, rows * 256);
@@ -154,6 +198,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
     }
   };
   auto store_tile = [&](int buf) {
+    const int skey = tid_o >> 4, sc = tid_o & 15;
+    const bool odd = (skey & 1) != 0;
+    const int vch = 4 * sc + 2 * (int)odd, vpos = v_position(skey & ~1);
     u32x2 kw = kh, vw = vh;
     if constexpr (!XH) {
       float4 x = kx;
@@ -173,17 +220,20 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
         __builtin_amdgcn_perm(hi, lo, 0x07060302u);
   };
 
-  // This wave's queries as B fragments of S^T = K.Q^T: fragment ds = query q0 + (l % 32),
-  // channels 16 ds + 8 (l / 32) .. + 7, rotated, times log2(e) (fp32 inputs), fp16. Rows are
-  // read whole (16 lanes per 256-byte fp32 row, 8 per 128-byte fp16 row) into the wave's LDS
-  // rows and read back in fragment order.
-  u32x4 qf[4];
-  if (active) {
-    unsigned char* Q = lds_q[wave];
+  // Query rows q0 .. q0 + 31 of (row0, head h); the buffer range ends at row T - 1, so rows
+  // past the sequence read as zeros.
+  auto query_rsrc = [&](long row0, int h, int q0) {
     const unsigned rows = (unsigned)(T - q0);
-    const rsrc_t qr = make_rsrc(reinterpret_cast<const unsigned char*>(p.q) +
-                                    ((row0 + (long)q0 * ts) * p.ldq + h * 64) * kEsz,
-                                (rows - 1) * ldq4 + kRowBytes);
+    return make_rsrc(reinterpret_cast<const unsigned char*>(p.q) +
+                         ((row0 + (long)q0 * ts) * p.ldq + h * 64) * kEsz,
+                     (rows - 1) * ldq4 + kRowBytes);
+  };
+  // This wave's 32 query rows, rotated, times log2(e) (fp32 inputs), fp16, into its LDS rows;
+  // all at once (the first pass of the walk, and sequences too short to prefetch).
+  auto stage_queries = [&](long row0, int h, int q0) {
+    unsigned char* Q = lds_q[wave];
+    const rsrc_t qr = query_rsrc(row0, h, q0);
+    const unsigned rows = (unsigned)(T - q0);
     if constexpr (XH) {
 #pragma unroll
       for (int it = 0; it < 4; it++) {
@@ -207,148 +257,252 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
             u32x2{pack_h2(x.x, x.y), pack_h2(x.z, x.w)};
       }
     }
-    // LDS operations of one wave complete in order: the reads see the rows just written.
-#pragma unroll
-    for (int ds = 0; ds < 4; ds++) qf[ds] = lds16(Q + row_offset(col, 2 * ds + half));
-  }
-
-  const int ntiles = (T + 63) / 64;
-  load_tile(0);
-  store_tile(0);
-  __builtin_amdgcn_s_waitcnt(kWaitVmem);
-  __syncthreads();
-
-  // Per-lane LDS offsets: K fragment (kb, ds) = keys 32 kb + (l % 32), chunk 2 ds + l / 32;
-  // V^T fragment (db, kb, k2) = channel 32 db + (l % 32), chunk 4 kb + 2 k2 + l / 32.
-  // Both are chunk 2 i + l / 32 of row l % 32 (i = ds, or 2 kb + k2), plus 4096 per 32 rows.
-  int fq[4];
-#pragma unroll
-  for (int i = 0; i < 4; i++) fq[i] = row_offset(col, 2 * i + half);
-
-  f32x16 o[2];  // O^T: channel 32 db + 8 i + 4 (l / 32) + e of query l % 32 in o[db][4 i + e]
-  o[0] = mfma32_zero();
-  o[1] = mfma32_zero();
-  float negm = 0.f, lsum = 0.f;  // -(running maximum), this lane's share of the row sum
-  if (active) {
-    // The running maximum starts at the exact maximum over the first 32 keys (T > 64).
-    f32x16 s = mfma32_zero();
-#pragma unroll
-    for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(lds_k[0] + fq[ds]), qf[ds], s);
-    float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[r]), s[r + 1]);
-    negm = -pair_max(fmaxf(mx, s[15]));
-  }
-
-  // One 32-key block kb of the tile in buffer buf. MASK: keys at or past T may be present.
-  auto block = [&](auto mask_tag, int buf, int kb, int key0) {
-    constexpr bool MASK = decltype(mask_tag)::value;
-    const unsigned char* K = lds_k[buf] + kb * 4096;
-    u32x4 kf[4];
-#pragma unroll
-    for (int ds = 0; ds < 4; ds++) kf[ds] = lds16(K + fq[ds]);
-    f32x16 s = seed16(negm);
-#pragma unroll
-    for (int ds = 0; ds < 4; ds++) s = mfma32(kf[ds], qf[ds], s);
-    // All four K reads in flight before the first MFMA waits on one.
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
-    if constexpr (MASK) {
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-#pragma unroll
-        for (int e = 0; e < 4; e++)
-          if (key0 + 32 * kb + 8 * i + 4 * half + e >= T) s[4 * i + e] = kMasked;
-    }
-    float lm = fmaxf(fmaxf(s[0], s[1]), s[2]);
-#pragma unroll
-    for (int r = 3; r < 15; r += 2) lm = fmaxf(fmaxf(lm, s[r]), s[r + 1]);
-    lm = fmaxf(lm, s[15]);
-    if (__builtin_amdgcn_uicmp(lm > kTau, 0, 33)) {
-      const float cm = pair_max(lm);
-      if (cm > kTau) {
-        const float alpha = fast_exp2(-cm);
-        negm -= cm;
-        s -= cm;
-        o[0] *= alpha;
-        o[1] *= alpha;
-        lsum *= alpha;
+  };
+  // Chunk c of the prefetch: direct-to-LDS loads, completed by the step's vmcnt wait.
+  auto issue_chunk = [&](long row0, int h, int q0, int c) {
+    int lane = tid & 63;
+    asm volatile("" : "+v"(lane));
+    const rsrc_t qr = query_rsrc(row0, h, q0);
+    if constexpr (XH) {
+      // Rows 8 c .. 8 c + 7 straight into their swizzled place: LDS slot l of the chunk holds
+      // row 8 c + l / 8, stored chunk l % 8 = logical chunk (l % 8) ^ ((row >> 1) & 7).
+      const int r = 8 * c + (lane >> 3);
+      const int cc = (lane & 7) ^ ((r >> 1) & 7);
+      load_lds16(qr, lds_q[wave] + 1024 * c, (unsigned)r * ldq4 + cc * 16);
+    } else {
+      // Rows 4 c + l / 16, 16-byte piece l % 16: query row, then cos and sin table rows.
+      const int r = 4 * c + (lane >> 4), cc = lane & 15;
+      unsigned char* R = lds_raw[wave];
+      load_lds16(qr, R, (unsigned)r * ldq4 + cc * 16);
+      if constexpr (ROPE) {
+        const unsigned rows = (unsigned)(T - q0);
+        const rsrc_t cr = make_rsrc(p.rope + (long)q0 * 64, rows * 256);
+        const rsrc_t sr = make_rsrc(p.rope + (long)(T + q0) * 64, rows * 256);
+        load_lds16(cr, R + 1024, (unsigned)r * 256 + cc * 16);
+        load_lds16(sr, R + 2048, (unsigned)r * 256 + cc * 16);
       }
     }
-#pragma unroll
-    for (int r = 0; r < 16; r++) s[r] = fast_exp2(s[r]);
-    u32x4 pf[2];
-#pragma unroll
-    for (int k2 = 0; k2 < 2; k2++) {
-      pf[k2] = u32x4{pack_h2(s[8 * k2], s[8 * k2 + 1]), pack_h2(s[8 * k2 + 2], s[8 * k2 + 3]),
-                     pack_h2(s[8 * k2 + 4], s[8 * k2 + 5]), pack_h2(s[8 * k2 + 6], s[8 * k2 + 7])};
-#pragma unroll
-      for (int d = 0; d < 4; d++) lsum = add_halves(pf[k2][d], lsum);
+  };
+  // fp32: rotate, scale and pack the landed chunk into the wave's fp16 query rows.
+  auto convert_chunk = [&](int c) {
+    if constexpr (!XH) {
+      int lane = tid & 63;
+      asm volatile("" : "+v"(lane));
+      const int r = 4 * c + (lane >> 4), cc = lane & 15;
+      const unsigned char* R = lds_raw[wave];
+      float4 x = __builtin_bit_cast(float4, lds16(R + 16 * lane));
+      if constexpr (ROPE)
+        x = rotate4(x, __builtin_bit_cast(float4, lds16(R + 1024 + 16 * lane)),
+                    __builtin_bit_cast(float4, lds16(R + 2048 + 16 * lane)));
+      x = scale4(x, kLog2e);
+      *reinterpret_cast<u32x2*>(lds_q[wave] + row_offset(r, cc >> 1) + ((cc & 1) << 3)) =
+          u32x2{pack_h2(x.x, x.y), pack_h2(x.z, x.w)};
     }
-    const unsigned char* V = lds_v[buf];
-#pragma unroll
-    for (int k2 = 0; k2 < 2; k2++)
-#pragma unroll
-      for (int db = 0; db < 2; db++)
-        o[db] = mfma32(lds16(V + db * 4096 + fq[2 * kb + k2]), pf[k2], o[db]);
   };
 
-  for (int j = 0; j + 1 < ntiles; j++) {
-    load_tile((j + 1) * 64);
-    if (active) {
-      block(std::false_type{}, j & 1, 0, j * 64);
-      block(std::false_type{}, j & 1, 1, j * 64);
-    }
-    store_tile((j + 1) & 1);
+  // Prologue of the walk: the first pass's queries and first K / V tile.
+  {
+    const int pi = (int)pass_of(0);
+    const int qblk = pi % qblocks, gh = pi / qblocks;
+    const int h = gh % p.heads, g = gh / p.heads;
+    const long row0 = group_row(p, g);
+    const int q0 = qblk * kQueries + wave * 32;
+    if (q0 < T) stage_queries(row0, h, q0);
+    load_tile(reinterpret_cast<const unsigned char*>(p.k) + (row0 * p.ldk + h * 64) * kEsz,
+              reinterpret_cast<const unsigned char*>(p.v) + (row0 * p.ldv + h * 64) * kEsz, 0, 0);
+    store_tile(0);
     __builtin_amdgcn_s_waitcnt(kWaitVmem);
     __syncthreads();
   }
-  if (!active) return;
-  {
-    const int j = ntiles - 1;
-    if (T % 64) {
-      block(std::true_type{}, j & 1, 0, j * 64);
-      if (T - j * 64 > 32) block(std::true_type{}, j & 1, 1, j * 64);
-    } else {
-      block(std::false_type{}, j & 1, 0, j * 64);
-      block(std::false_type{}, j & 1, 1, j * 64);
-    }
-  }
 
-  // Epilogue: 1/l (and the gate), then this lane's channels 32 db + 8 i + 4 (l / 32) .. + 3 of
-  // query q0 + (l % 32). Rows at or past T are dropped by the range check.
-  const OutRows out = out_rows(p, g, h);
-  const int t = q0 + col;
-  float scale = 1.0f / pair_sum(lsum);
-  if constexpr (GATED) {
-    const float gl =
-        out.gate_half
-            ? (float)__builtin_bit_cast(_Float16, __builtin_amdgcn_raw_buffer_load_b16(
-                                                      out.gate, (unsigned)t * out.ldg4, 0, 0))
-            : bload1(out.gate, (unsigned)t * out.ldg4);
-    scale = scale / (1.0f + expf(-gl));
-  }
+  int buf = 0;  // LDS buffer holding the current tile
+  for (int rnd = 0;; rnd++) {
+    const long pl = pass_of(rnd);
+    if (pl >= passes) break;
+    const int pi = (int)pl;
+    const long pnl = pass_of(rnd + 1);
+    const bool has_next = pnl < passes;
+    const int pn = has_next ? (int)pnl : pi;
+    T = p.tokens;
+    lane = tid & 63;
+    tid_o = tid;
+    asm volatile("" : "+s"(T), "+s"(ldq4), "+s"(ldk4), "+s"(ldv4), "+v"(lane), "+v"(tid_o));
+    const int half = lane >> 5, col = lane & 31;
+
+    const int qblk = pi % qblocks, gh = pi / qblocks;
+    const int h = gh % p.heads, g = gh / p.heads;
+    const long row0 = group_row(p, g);
+    const unsigned char* kbase =
+        reinterpret_cast<const unsigned char*>(p.k) + (row0 * p.ldk + h * 64) * kEsz;
+    const unsigned char* vbase =
+        reinterpret_cast<const unsigned char*>(p.v) + (row0 * p.ldv + h * 64) * kEsz;
+    const int q0 = qblk * kQueries + wave * 32;
+    const bool active = q0 < T;
+    // The next pass (this workgroup's next round).
+    const int qblkn = pn % qblocks, ghn = pn / qblocks;
+    const int hn = ghn % p.heads, gn = ghn / p.heads;
+    const long row0n = group_row(p, gn);
+    const int q0n = qblkn * kQueries + wave * 32;
+    const bool active_n = has_next && q0n < T;
+    // The prefetch takes the last kCh K / V steps of the pass.
+    const bool prefetch = active_n && ntiles - 1 >= kCh;
+    const int cstart = ntiles - 1 - kCh;
+
+    // This wave's queries as B fragments of S^T = K.Q^T: fragment ds = query q0 + (l % 32),
+    // channels 16 ds + 8 (l / 32) .. + 7. LDS operations of one wave complete in order: these
+    // reads see the rows staged before, and precede this pass's prefetch into the same rows.
+    // Per-lane LDS offsets: K fragment (kb, ds) = keys 32 kb + (l % 32), chunk 2 ds + l / 32;
+    // V^T fragment (db, kb, k2) = channel 32 db + (l % 32), chunk 4 kb + 2 k2 + l / 32. Both are
+    // chunk 2 i + l / 32 of row l % 32 (i = ds, or 2 kb + k2), plus 4096 per 32 rows.
+    int fq[4];
 #pragma unroll
-  for (int db = 0; db < 2; db++)
+    for (int i = 0; i < 4; i++) fq[i] = row_offset(col, 2 * i + half);
+    u32x4 qf[4];
+    if (active) {
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
-      const unsigned c = (unsigned)(32 * db + 8 * i + 4 * half);
-      const float4 v = make_float4(o[db][4 * i] * scale, o[db][4 * i + 1] * scale,
-                                   o[db][4 * i + 2] * scale, o[db][4 * i + 3] * scale);
-      if (out.half)
-        __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)},
-                                              out.out, (unsigned)t * out.ld4 + c * 2, 0, 0);
-      else
-        bstore4<true>(out.out, (unsigned)t * out.ld4 + c * 4, v);
+      for (int ds = 0; ds < 4; ds++) qf[ds] = lds16(lds_q[wave] + fq[ds]);
     }
+
+    f32x16 o[2];  // O^T: channel 32 db + 8 i + 4 (l / 32) + e of query l % 32 in o[db][4 i + e]
+    o[0] = zero16();
+    o[1] = zero16();
+    float negm = 0.f, lsum = 0.f;  // -(running maximum), this lane's share of the row sum
+    if (active) {
+      // The running maximum starts at the exact maximum over the first 32 keys (T > 64).
+      f32x16 s = zero16();
+#pragma unroll
+      for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(lds_k[buf] + fq[ds]), qf[ds], s);
+      float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[r]), s[r + 1]);
+      negm = -pair_max(fmaxf(mx, s[15]));
+    }
+
+    // One 32-key block kb of the tile in buffer b. MASK: keys at or past T may be present.
+    auto block = [&](auto mask_tag, int b, int kb, int key0) {
+      constexpr bool MASK = decltype(mask_tag)::value;
+      const unsigned char* K = lds_k[b] + kb * 4096;
+      f32x16 s = seed16(negm);
+#pragma unroll
+      for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(K + fq[ds]), qf[ds], s);
+      if constexpr (MASK) {
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int e = 0; e < 4; e++)
+            if (key0 + 32 * kb + 8 * i + 4 * half + e >= T) s[4 * i + e] = kMasked;
+      }
+      float lm = fmaxf(fmaxf(s[0], s[1]), s[2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) lm = fmaxf(fmaxf(lm, s[r]), s[r + 1]);
+      lm = fmaxf(lm, s[15]);
+      if (__builtin_amdgcn_uicmp(lm > kTau, 0, 33)) {
+        const float cm = pair_max(lm);
+        if (cm > kTau) {
+          const float alpha = fast_exp2(-cm);
+          negm -= cm;
+          s -= cm;
+          o[0] *= alpha;
+          o[1] *= alpha;
+          lsum *= alpha;
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < 16; r++) s[r] = fast_exp2(s[r]);
+      u32x4 pf[2];
+#pragma unroll
+      for (int k2 = 0; k2 < 2; k2++) {
+        pf[k2] = u32x4{pack_h2(s[8 * k2], s[8 * k2 + 1]), pack_h2(s[8 * k2 + 2], s[8 * k2 + 3]),
+                       pack_h2(s[8 * k2 + 4], s[8 * k2 + 5]), pack_h2(s[8 * k2 + 6], s[8 * k2 + 7])};
+#pragma unroll
+        for (int d = 0; d < 4; d++) lsum = add_halves(pf[k2][d], lsum);
+      }
+      const unsigned char* V = lds_v[b];
+#pragma unroll
+      for (int k2 = 0; k2 < 2; k2++)
+#pragma unroll
+        for (int db = 0; db < 2; db++)
+          o[db] = mfma32(lds16(V + db * 4096 + fq[2 * kb + k2]), pf[k2], o[db]);
+    };
+
+    for (int j = 0; j + 1 < ntiles; j++) {
+      // The next tile's K / V rows first; its table rows and the query chunk after the first
+      // block, so that the 16 waves' loads do not all queue at the start of the step.
+      load_tile(kbase, vbase, (j + 1) * 64, 1);
+      const int c = j - cstart;
+      if (active) block(std::false_type{}, buf, 0, j * 64);
+      load_tile(kbase, vbase, (j + 1) * 64, 2);
+      if (prefetch && c >= 0) issue_chunk(row0n, hn, q0n, c);
+      if (active) block(std::false_type{}, buf, 1, j * 64);
+      __builtin_amdgcn_s_waitcnt(kWaitVmem);
+      if (prefetch && c >= 0) convert_chunk(c);
+      store_tile(buf ^ 1);
+      __syncthreads();
+      buf ^= 1;
+    }
+
+    // Last tile of this pass (keys at or past T masked; a fully masked block adds zeros). The
+    // next pass's first tile loads after its blocks, beside this pass's epilogue.
+    if (active) {
+      const int j = ntiles - 1;
+      block(std::true_type{}, buf, 0, j * 64);
+      block(std::true_type{}, buf, 1, j * 64);
+    }
+    if (has_next)
+      load_tile(reinterpret_cast<const unsigned char*>(p.k) + (row0n * p.ldk + hn * 64) * kEsz,
+                reinterpret_cast<const unsigned char*>(p.v) + (row0n * p.ldv + hn * 64) * kEsz,
+                0, 0);
+    float scale = 0.f, gl = 0.f;
+    const OutRows out = out_rows(p, g, h);
+    if (active) {
+      scale = 1.0f / pair_sum(lsum);
+      if constexpr (GATED) {
+        const int t = q0 + col;
+        gl = out.gate_half ? (float)__builtin_bit_cast(
+                                 _Float16, __builtin_amdgcn_raw_buffer_load_b16(
+                                               out.gate, (unsigned)t * out.ldg4, 0, 0))
+                           : bload1(out.gate, (unsigned)t * out.ldg4);
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitVmem);
+    if (has_next) store_tile(buf ^ 1);
+    if (active_n && !prefetch) stage_queries(row0n, hn, q0n);
+    if (active) {
+      // Epilogue: 1/l (and the gate), then this lane's channels 32 db + 8 i + 4 (l / 32) .. + 3
+      // of query q0 + (l % 32). Rows at or past T are dropped by the range check. Issued after
+      // the wait above, so the stores drain while the next pass runs.
+      if constexpr (GATED) scale = scale / (1.0f + expf(-gl));
+      const int t = q0 + col;
+#pragma unroll
+      for (int db = 0; db < 2; db++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const unsigned c = (unsigned)(32 * db + 8 * i + 4 * half);
+          const float4 v = make_float4(o[db][4 * i] * scale, o[db][4 * i + 1] * scale,
+                                       o[db][4 * i + 2] * scale, o[db][4 * i + 3] * scale);
+          if (out.half)
+            __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)},
+                                                  out.out, (unsigned)t * out.ld4 + c * 2, 0, 0);
+          else
+            bstore4<true>(out.out, (unsigned)t * out.ld4 + c * 4, v);
+        }
+    }
+    // The next pass's first tile and query rows are in place; this pass's tiles are free.
+    __syncthreads();
+    buf ^= 1;
+  }
 }
 
 template <bool GATED, bool ROPE, bool XH>
 hipError_t launch_t(const AttnParams& p, hipStream_t stream) {
   const int qblocks = (p.tokens + kQueries - 1) / kQueries;
-  const int total = p.groups * p.heads * qblocks;
-  hipLaunchKernelGGL((attention_long_kernel<GATED, ROPE, XH>), dim3(total), dim3(kWaves * 64), 0,
-                     stream, p, qblocks, total);
+  const int passes = p.groups * p.heads * qblocks;
+  // One workgroup per CU walks the passes when there are more than two rounds of them; fewer
+  // passes run one per workgroup (the walk would only lengthen the critical path).
+  const int cus = device_cus();
+  const int grid = passes <= 2 * cus ? passes : cus;
+  hipLaunchKernelGGL((attention_long_kernel<GATED, ROPE, XH>), dim3(grid), dim3(kWaves * 64), 0,
+                     stream, p, qblocks, passes);
   return hipGetLastError();
 }
 
