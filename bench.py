@@ -10,9 +10,11 @@ inputs resident in HBM.
 Prints ONE JSON line: throughput in TFLOP/s (4*G*H*T^2*d per call), the live roofline of the
 attention kernel (HIP events over the timed region on the launch stream) and the restated
 reference CPU path (the oracle's materialized-tile attention) timed on the host's cores. The
-same line carries, under "mel_roformer", the second half of the headline metric: the
-audio-seconds per second of the Mel-RoFormer separation of a 30 s clip (as `--workload mel`
-measures it, with its own roofline and CPU baseline).
+same line carries the path's other configurations, each as its `--workload` measures it with
+its own roofline and CPU baseline: "band_attention" (the band-axis op), "layer_pair" (one
+RoFormer layer pair), "mel_roformer" (the second half of the headline metric: audio-seconds per
+second of the Mel-RoFormer separation of a 30 s clip) and "bs_roformer_large" (BS-RoFormer-large
+on a 5 min clip). `--no-extra` / `--no-mel` leave sections out.
 
 `--workload band` measures the band-axis op [1602, 60, 8, 64] instead (HBM-bound roofline),
 `--workload layer` one RoFormer layer pair on [2, 60, 801, 384], and `--workload mel` the
@@ -158,6 +160,12 @@ def layer_flops(groups, tokens, dim, heads, hidden):
 
 
 def run_layer(args, torch, dev) -> int:
+    print(json.dumps(layer_result(args.steps, args.warmup, args.no_cpu_baseline, torch, dev)),
+          flush=True)
+    return 0
+
+
+def layer_result(steps, warmup, no_cpu_baseline, torch, dev) -> dict:
     """One RoFormer layer pair (time pass then band pass) on x [2, 60, 801, 384]."""
     from ancha_amd import roformer
     from ancha_amd import workload as W
@@ -171,19 +179,19 @@ def run_layer(args, torch, dev) -> int:
     tb = roformer.axis_rope(wb["freqs"], NB, dev)
     step = lambda: pair(x, tt, tb)
     out = step()
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         out = step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         out = step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    gpu_ms = start.elapsed_time(end) / args.steps
+    gpu_ms = start.elapsed_time(end) / steps
     flops_time = layer_flops(B * NB, T, D, c["heads"], c["hidden"])
     flops_band = layer_flops(B * T, NB, D, c["heads"], c["hidden"])
     flops = flops_time + flops_band
@@ -191,9 +199,9 @@ def run_layer(args, torch, dev) -> int:
     log(f"layer pair: {gpu_ms:.3f} ms/step, {achieved:.1f} TFLOP/s")
     result = {
         "metric": "RoFormer layer pair TFLOP/s (% MFMA peak)",
-        "value": round(flops * args.steps / wall / 1e12, 3),
-        "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 4), "higher_is_better": True,
+        "value": round(flops * steps / wall / 1e12, 3),
+        "unit": "TFLOP/s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
         "data": "synthetic: x ~ N(0,1), weights ~ N(0,0.02), gamma = 1 (seeded)",
         "config": {"workload": "RoFormer layer pair: time pass on [120, 801, 384] then band "
@@ -205,11 +213,11 @@ def run_layer(args, torch, dev) -> int:
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
                      "traffic": None, "scope": "whole layer pair (all kernels)"},
     }
-    if not args.no_cpu_baseline:
+    if not no_cpu_baseline:
         log("timing the restated reference CPU path (Burn-path block) on sampled groups")
         result["cpu_baseline"] = layer_cpu_baseline(wt, wb, x, out)
-    print(json.dumps(result), flush=True)
-    return 0
+    del out, x, pair
+    return result
 
 
 def layer_cpu_baseline(wt, wb, x, gpu_out, budget_s: float = 12.0) -> dict:
@@ -392,6 +400,11 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-mel", action="store_true",
                     help="time workload: leave out the Mel-RoFormer 30 s separation section")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="time workload: leave out the band-op, layer-pair and BS-RoFormer-large "
+                         "sections")
+    ap.add_argument("--bs-steps", type=int, default=2,
+                    help="timed clips of the BS-RoFormer-large section of the time workload")
     ap.add_argument("--mel-steps", type=int, default=5,
                     help="timed clips of the Mel-RoFormer section of the time workload")
     ap.add_argument("--mel-warmup", type=int, default=1)
@@ -412,7 +425,6 @@ def main() -> int:
     import torch
 
     from ancha_amd import fused
-    from ancha_amd import workload as W
 
     if not torch.cuda.is_available() or not fused.available():
         print("bench.py needs an MI355X (gfx950) GPU and the built kernel library",
@@ -423,18 +435,51 @@ def main() -> int:
         return run_layer(args, torch, dev)
     if args.workload in SEPARATIONS:
         return run_separation(args, torch, dev)
-    shape = W.TIME_SHAPE if args.workload == "time" else W.BAND_SHAPE
-    if args.tokens is not None:
-        if not 1 <= args.tokens <= 8192:
-            print("--tokens must be in [1, 8192]", file=sys.stderr)
-            return 2
-        shape = (shape[0], args.tokens, shape[2], shape[3])
+    if args.tokens is not None and not 1 <= args.tokens <= 8192:
+        print("--tokens must be in [1, 8192]", file=sys.stderr)
+        return 2
+    result = attention_result(args.workload, args.steps, args.warmup, args.no_cpu_baseline,
+                              args.tokens, args.copy_calibration, torch, dev)
+    if result is None:
+        return 0
+    if args.workload == "time" and args.tokens is None:
+        # The other configurations of the path, each with its own roofline (and CPU baseline),
+        # in the same JSON line: the band-axis op, one layer pair, and the second half of the
+        # headline metric, the Mel-RoFormer separation of a 30 s clip; BS-RoFormer-large last.
+        if not args.no_extra:
+            log("band-axis op [1602, 60, 8, 64]")
+            result["band_attention"] = attention_result(
+                "band", args.steps, args.warmup, args.no_cpu_baseline, None, False, torch, dev)
+            log("layer pair [2, 60, 801, 384]")
+            result["layer_pair"] = layer_result(args.steps, min(args.warmup, 10),
+                                                args.no_cpu_baseline, torch, dev)
+        if not args.no_mel:
+            log("Mel-RoFormer separation of a 30 s clip")
+            result["mel_roformer"] = separation_result("mel", args.mel_steps, args.mel_warmup,
+                                                       args.no_cpu_baseline, torch, dev)
+        if not args.no_extra:
+            log("BS-RoFormer-large separation of a 5 min clip")
+            result["bs_roformer_large"] = separation_result(
+                "bs", args.bs_steps, 1, args.no_cpu_baseline, torch, dev)
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def attention_result(workload, steps, warmup, no_cpu_baseline, tokens, copy_cal, torch, dev):
+    """The fused attention op on q, k, v resident in HBM: the time-axis shape (MFMA roofline)
+    or the band-axis shape (HBM roofline), RoPE on load."""
+    from ancha_amd import fused
+    from ancha_amd import workload as W
+    shape = W.TIME_SHAPE if workload == "time" else W.BAND_SHAPE
+    if tokens is not None:
+        shape = (shape[0], tokens, shape[2], shape[3])
     G, T, H, D = shape
-    default_shape = args.tokens is None
+    default_shape = tokens is None
     log(f"generating q, k, v {shape} on the GPU")
     q, k, v = (W.normal_torch(shape, s, 1.0 / 8.0, device=dev) for s in (1, 2, 3))
-    if args.copy_calibration:
-        return copy_calibration(torch, dev, G * T * H * D * 2, args.steps)
+    if copy_cal:
+        copy_calibration(torch, dev, G * T * H * D * 2, steps)
+        return None
     table_np = W.axis_rope_packed(W.rope_freqs(), T)
     table = torch.from_numpy(table_np).to(dev)
     torch.cuda.synchronize()
@@ -444,25 +489,25 @@ def main() -> int:
 
     out = step()
     assert out is not None, "attention kernel rejected the workload"
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         out = step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     start.record(stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         out = step()
     end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = start.elapsed_time(end) / args.steps
+    kernel_ms = start.elapsed_time(end) / steps
     flops = 4.0 * G * H * T * T * D
     io_bytes = 4.0 * 4 * G * T * H * D  # q, k, v read + out written, fp32
-    value = flops * args.steps / wall / 1e12
-    log(f"{args.workload}: {kernel_ms * 1e3:.1f} us/launch, {flops / kernel_ms / 1e9:.1f} TFLOP/s, "
+    value = flops * steps / wall / 1e12
+    log(f"{workload}: {kernel_ms * 1e3:.1f} us/launch, {flops / kernel_ms / 1e9:.1f} TFLOP/s, "
         f"{io_bytes / kernel_ms / 1e6:.0f} GB/s")
-    if args.workload == "time":
+    if workload == "time":
         achieved = flops / (kernel_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
@@ -477,33 +522,26 @@ def main() -> int:
         "value": round(value, 3),
         "unit": "TFLOP/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
-        "ms_per_step": round(wall * 1e3 / args.steps, 4),
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(wall * 1e3 / steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16",
         "data": "synthetic: seeded N(0,1)/8 q, k, v (splitmix64 + Box-Muller)",
-        "config": {"workload": f"{args.workload}-axis fused attention, RoPE on load",
+        "config": {"workload": f"{workload}-axis fused attention, RoPE on load",
                    "groups": G, "tokens": T, "heads": H, "head_dim": D,
                    "io": "fp32", "mfma_operands": "fp16", "accumulate": "fp32",
                    "parallelism": "single GPU"},
         "roofline": roofline,
     }
-    if not args.no_cpu_baseline:
+    if not no_cpu_baseline:
         log("timing the restated reference CPU path")
         result["cpu_baseline"] = cpu_baseline(q.cpu().numpy(), k.cpu().numpy(),
                                               v.cpu().numpy(), table_np, out.cpu().numpy())
-    if args.workload == "time" and not args.no_mel:
-        # The second half of the headline metric: audio-seconds/sec of the Mel-RoFormer
-        # separation of a 30 s clip, in the same JSON line.
-        del q, k, v, out
-        log("Mel-RoFormer separation of a 30 s clip")
-        result["mel_roformer"] = separation_result("mel", args.mel_steps, args.mel_warmup,
-                                                   args.no_cpu_baseline, torch, dev)
-    print(json.dumps(result), flush=True)
-    return 0
+    del q, k, v, out
+    return result
 
 
 if __name__ == "__main__":
