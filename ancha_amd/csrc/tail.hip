@@ -38,6 +38,9 @@ constexpr int kRows = 64;         // rows per workgroup step
 constexpr int kChunk = 128;       // hidden units per chunk
 constexpr int kWaves = 4;         // one per feature quarter (and per SIMD)
 constexpr int kFrag = 1024;       // bytes of one 32 x 16 fp16 fragment
+// B fragments are read from LDS this many k steps ahead of their MFMAs (a scheduling barrier
+// per step keeps the reads there), so an MFMA never waits on a read issued just before it.
+constexpr int kBD = 2;
 
 // Lane l's B fragment (8 halves) from accumulator values 8 sub .. 8 sub + 7 (q = 2 sub, 2 sub + 1).
 __device__ __forceinline__ u32x4 pack_frag(const f32x16& d, int sub, float s) {
@@ -143,20 +146,26 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
       };
 #pragma unroll
       for (int s = 0; s < PD; s++) load_a(s, a[s]);
+      u32x4 b[kBD + 1][2];
+      auto load_b = [&](int s, u32x4 (&dst)[2]) {
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+          dst[j] = *reinterpret_cast<const u32x4*>(lds + ((2 * rh + j) * S0 + s) * kFrag + lane16);
+      };
+#pragma unroll
+      for (int s = 0; s < kBD; s++) load_b(s, b[s]);
 #pragma unroll
       for (int s = 0; s < S0; s++) {
         u32x4 cur[NI];
 #pragma unroll
         for (int i = 0; i < NI; i++) cur[i] = a[s % PD][i];
         if (s + PD < S0) load_a(s + PD, a[s % PD]);
-        u32x4 b[2];
-#pragma unroll
-        for (int j = 0; j < 2; j++)
-          b[j] = *reinterpret_cast<const u32x4*>(lds + ((2 * rh + j) * S0 + s) * kFrag + lane16);
+        if (s + kBD < S0) load_b(s + kBD, b[(s + kBD) % (kBD + 1)]);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int i = 0; i < NI; i++)
 #pragma unroll
-          for (int j = 0; j < 2; j++) acc[i][j] = mfma32(cur[i], b[j], acc[i][j]);
+          for (int j = 0; j < 2; j++) acc[i][j] = mfma32(cur[i], b[s % (kBD + 1)][j], acc[i][j]);
       }
     }
     __syncthreads();  // the attended tile is dead: X / H may be written
@@ -201,18 +210,24 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
         for (int s = 0; s < PD && s < SD; s++)
           a[s] = __builtin_amdgcn_raw_buffer_load_b128(w1, lane16,
                                                        (unsigned)((blk1 * SD + s) * kFrag), 0);
+        u32x4 b[kBD + 1][2];
+        auto load_b = [&](int s, u32x4 (&dst)[2]) {
+#pragma unroll
+          for (int j = 0; j < 2; j++)
+            dst[j] = *reinterpret_cast<const u32x4*>(X + ((2 * rh + j) * SD + s) * kFrag + lane16);
+        };
+#pragma unroll
+        for (int s = 0; s < kBD; s++) load_b(s, b[s]);
 #pragma unroll
         for (int s = 0; s < SD; s++) {
           const u32x4 cur = a[s % PD];
           if (s + PD < SD)
             a[s % PD] = __builtin_amdgcn_raw_buffer_load_b128(
                 w1, lane16, (unsigned)((blk1 * SD + s + PD) * kFrag), 0);
+          if (s + kBD < SD) load_b(s + kBD, b[(s + kBD) % (kBD + 1)]);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int j = 0; j < 2; j++)
-            hacc[j] = mfma32(cur,
-                             *reinterpret_cast<const u32x4*>(X + ((2 * rh + j) * SD + s) * kFrag +
-                                                             lane16),
-                             hacc[j]);
+          for (int j = 0; j < 2; j++) hacc[j] = mfma32(cur, b[s % (kBD + 1)][j], hacc[j]);
         }
       }
       // GELU(h + b1), fp16, into H as FF-out B fragments (hidden steps 2 fq, 2 fq + 1).
@@ -252,20 +267,26 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
         };
 #pragma unroll
         for (int s = 0; s < PD; s++) load_a(s, a[s]);
+        u32x4 b[kBD + 1][2];
+        auto load_b = [&](int s, u32x4 (&dst)[2]) {
+#pragma unroll
+          for (int j = 0; j < 2; j++)
+            dst[j] = *reinterpret_cast<const u32x4*>(H + ((2 * rh + j) * 8 + s) * kFrag + lane16);
+        };
+#pragma unroll
+        for (int s = 0; s < kBD; s++) load_b(s, b[s]);
 #pragma unroll
         for (int s = 0; s < 8; s++) {
           u32x4 cur[NI];
 #pragma unroll
           for (int i = 0; i < NI; i++) cur[i] = a[s % PD][i];
           if (s + PD < 8) load_a(s + PD, a[s % PD]);
-          u32x4 b[2];
-#pragma unroll
-          for (int j = 0; j < 2; j++)
-            b[j] = *reinterpret_cast<const u32x4*>(H + ((2 * rh + j) * 8 + s) * kFrag + lane16);
+          if (s + kBD < 8) load_b(s + kBD, b[(s + kBD) % (kBD + 1)]);
+          __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int i = 0; i < NI; i++)
 #pragma unroll
-            for (int j = 0; j < 2; j++) acc[i][j] = mfma32(cur[i], b[j], acc[i][j]);
+            for (int j = 0; j < 2; j++) acc[i][j] = mfma32(cur[i], b[s % (kBD + 1)][j], acc[i][j]);
         }
       }
     }
