@@ -18,16 +18,19 @@
 namespace ancha {
 namespace {
 
-constexpr int kSplitFrames = 16;   // frames per workgroup
+constexpr int kSplitFrames = 32;   // frames per workgroup
 constexpr int kSplitThreads = 256;
-constexpr int kSplitCols = 512;    // feature columns staged per pass (32 KB of LDS)
+constexpr int kSplitCols = 256;    // feature columns staged per pass (32 KB of LDS)
 constexpr int kSplitDims = 4;      // output channels per thread (one float4 of W')
+constexpr int kSplitHalf = kSplitFrames / 2;  // frames per thread job
 constexpr int kSplitJobs = 2 * 512 / kSplitDims;  // (channel group, frame half) pairs, dim <= 512
 
-// Thread job (dg, half): channels 4*dg .. 4*dg+3 for frames 8*half .. 8*half+7 of the tile.
+// Thread job (dg, half): channels 4*dg .. 4*dg+3 for frames 16*half .. 16*half+15 of the tile.
 // The band's features pass through LDS transposed, zt[column][frame], kSplitCols columns at a
-// time, so a thread reads its 8 frames of a column as two 16-byte words and its 4 weights as
-// one: 32 FMAs per 3 loads. Squared norms accumulate over the passes; 1/norm is applied last.
+// time, so a thread reads its 16 frames of a column as four 16-byte words and its 4 weights as
+// one: 64 FMAs per 5 loads. Squared norms accumulate over the passes; 1/norm is applied last.
+// 32 frames per workgroup amortise the gather of the band's spectrum columns (two dependent
+// global reads) over twice the arithmetic of a 16-frame tile.
 __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitParams p) {
   __shared__ __attribute__((aligned(16))) float zt[kSplitCols * kSplitFrames];
   __shared__ float sq[kSplitFrames];
@@ -36,14 +39,15 @@ __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitPara
   const int frames = min(kSplitFrames, p.frames - t0);
   const float* w = p.weight + (long)p.wofs[b] * p.dim;
   const int groups = p.dim / kSplitDims;
+  const int job = threadIdx.x;
+  const bool active = job < 2 * groups;
+  const int dg = job % groups, half = job / groups, d0 = kSplitDims * dg;
   if (threadIdx.x < kSplitFrames) sq[threadIdx.x] = 0.0f;
-  float acc[2][8][kSplitDims];  // the thread's (up to) two jobs
+  float acc[kSplitHalf][kSplitDims];
 #pragma unroll
-  for (int r = 0; r < 2; r++)
+  for (int i = 0; i < kSplitHalf; i++)
 #pragma unroll
-    for (int i = 0; i < 8; i++)
-#pragma unroll
-      for (int j = 0; j < kSplitDims; j++) acc[r][i][j] = 0.0f;
+    for (int j = 0; j < kSplitDims; j++) acc[i][j] = 0.0f;
   for (int c0 = 0; c0 < width; c0 += kSplitCols) {
     const int cols = min(kSplitCols, width - c0), bins = cols / 4;
     __syncthreads();  // the previous pass is done with zt
@@ -59,48 +63,47 @@ __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitPara
       zt[(4 * q + 3) * kSplitFrames + tt] = v.w;
     }
     __syncthreads();
-    {  // squared norms: 16 lanes per frame
-      const int tt = threadIdx.x >> 4, l = threadIdx.x & 15;
+    // squared norms: 16 lanes per frame
+    for (int tt = threadIdx.x >> 4; tt < kSplitFrames; tt += kSplitThreads / 16) {
+      const int l = threadIdx.x & 15;
       float s = 0.0f;
       for (int c = l; c < cols; c += 16) s += zt[c * kSplitFrames + tt] * zt[c * kSplitFrames + tt];
       for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o);
       if (l == 0) sq[tt] += s;
     }
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-      const int job = threadIdx.x + r * kSplitThreads;
-      if (job >= 2 * groups) break;
-      const int dg = job % groups, half = job / groups, d0 = kSplitDims * dg;
-      const float* zc = zt + half * 8;
+    if (active) {
+      const float* zc = zt + half * kSplitHalf;
       const float* wc = w + (long)c0 * p.dim + d0;
-#pragma unroll 4
+#pragma unroll 8
       for (int c = 0; c < cols; c++) {
         const float4 wv = *reinterpret_cast<const float4*>(wc + (long)c * p.dim);
-        const float4 za = *reinterpret_cast<const float4*>(zc + c * kSplitFrames);
-        const float4 zb = *reinterpret_cast<const float4*>(zc + c * kSplitFrames + 4);
-        const float zz[8] = {za.x, za.y, za.z, za.w, zb.x, zb.y, zb.z, zb.w};
+        float zz[kSplitHalf];
+#pragma unroll
+        for (int k = 0; k < kSplitHalf / 4; k++) {
+          const float4 z = *reinterpret_cast<const float4*>(zc + c * kSplitFrames + 4 * k);
+          zz[4 * k] = z.x;
+          zz[4 * k + 1] = z.y;
+          zz[4 * k + 2] = z.z;
+          zz[4 * k + 3] = z.w;
+        }
         const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-        for (int i = 0; i < 8; i++)
+        for (int i = 0; i < kSplitHalf; i++)
 #pragma unroll
-          for (int j = 0; j < kSplitDims; j++) acc[r][i][j] += ww[j] * zz[i];
+          for (int j = 0; j < kSplitDims; j++) acc[i][j] += ww[j] * zz[i];
       }
     }
   }
   __syncthreads();
-#pragma unroll
-  for (int r = 0; r < 2; r++) {
-    const int job = threadIdx.x + r * kSplitThreads;
-    if (job >= 2 * groups) break;
-    const int dg = job % groups, half = job / groups, d0 = kSplitDims * dg;
+  if (active) {
     const float4 bias = *reinterpret_cast<const float4*>(p.bias + (long)b * p.dim + d0);
-    for (int i = 0; i < 8; i++) {
-      const int tt = half * 8 + i;
+    for (int i = 0; i < kSplitHalf; i++) {
+      const int tt = half * kSplitHalf + i;
       if (tt >= frames) break;
       const float s = 1.0f / fmaxf(sqrtf(sq[tt]), 1e-12f);
       *reinterpret_cast<float4*>(p.x + ((long)b * p.frames + t0 + tt) * p.dim + d0) =
-          make_float4(acc[r][i][0] * s + bias.x, acc[r][i][1] * s + bias.y,
-                      acc[r][i][2] * s + bias.z, acc[r][i][3] * s + bias.w);
+          make_float4(acc[i][0] * s + bias.x, acc[i][1] * s + bias.y, acc[i][2] * s + bias.z,
+                      acc[i][3] * s + bias.w);
     }
   }
 }
