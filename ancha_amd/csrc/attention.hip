@@ -156,6 +156,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
   const unsigned toff = (unsigned)lrow * 256 + lchunk * 16;
   float4 kreg[2], vreg[2];
   float4 kcos[2], ksin[2];
+  int tile_key0 = 0;
   // fp16 staging: thread owns the 16-byte chunk tid & 7 of K row tid >> 3, and the same V
   // block as above as two 8-byte rows.
   u32x4 kh;
@@ -177,16 +178,20 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
     for (int it = 0; it < 2; it++) kreg[it] = bload4<ALIGNED>(kr, koff + it * 32 * ldk4);
 #pragma unroll
     for (int r = 0; r < 2; r++) vreg[r] = bload4<ALIGNED>(vr, voff + r * ldv4);
-    if constexpr (ROPE) {
-      // Key cos rows (table 2) and +sin values (odd channels of table 3) of this tile.
-      const rsrc_t cr = make_rsrc(p.rope + (long)(2 * T + key0) * 64, rows * 256);
-      const rsrc_t sr = make_rsrc(p.rope + (long)(3 * T + key0) * 64, rows * 256);
+    tile_key0 = key0;
+  };
+  // Key cos rows (table 2) and +sin values (odd channels of table 3) of the staged tile, read
+  // when the tile is stored (not a tile ahead: this kernel serves rows that are not 16-byte
+  // aligned, and the table registers held across the tile's compute would spill).
+  auto load_table = [&]() {
+    const unsigned rows = (unsigned)(T - tile_key0);
+    const rsrc_t cr = make_rsrc(p.rope + (long)(2 * T + tile_key0) * 64, rows * 256);
+    const rsrc_t sr = make_rsrc(p.rope + (long)(3 * T + tile_key0) * 64, rows * 256);
 #pragma unroll
-      for (int it = 0; it < 2; it++) {
-        const unsigned o = toff + it * 32 * 256;
-        kcos[it] = bload4<ALIGNED>(cr, o);
-        ksin[it] = bload4<ALIGNED>(sr, o);
-      }
+    for (int it = 0; it < 2; it++) {
+      const unsigned o = toff + it * 32 * 256;
+      kcos[it] = bload4<ALIGNED>(cr, o);
+      ksin[it] = bload4<ALIGNED>(sr, o);
     }
   };
   auto store_tile = [&](int buf) {
@@ -198,6 +203,7 @@ __global__ __launch_bounds__(kTimeWaves * 64) void attention_time_kernel(AttnPar
             v_pair(vh[0], vh[1], j);
       return;
     }
+    if constexpr (ROPE) load_table();
 #pragma unroll
     for (int it = 0; it < 2; it++) {
       const int r = lrow + 32 * it;
@@ -704,11 +710,14 @@ static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
     }
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, stream, p, problems);
   } else {
-    if constexpr (ALIGNED) return launch_attention_long(p, GATED, ROPE, stream);
-    const int qblocks = (T + kTimeQueries - 1) / kTimeQueries;
-    const int total = p.groups * p.heads * qblocks;
-    hipLaunchKernelGGL((attention_time_kernel<GATED, ROPE, ALIGNED, XH>), dim3(total),
-                       dim3(kTimeWaves * 64), 0, stream, p, qblocks, total);
+    if constexpr (ALIGNED) {
+      return launch_attention_long(p, GATED, ROPE, stream);
+    } else {
+      const int qblocks = (T + kTimeQueries - 1) / kTimeQueries;
+      const int total = p.groups * p.heads * qblocks;
+      hipLaunchKernelGGL((attention_time_kernel<GATED, ROPE, ALIGNED, XH>), dim3(total),
+                         dim3(kTimeWaves * 64), 0, stream, p, qblocks, total);
+    }
   }
   return hipGetLastError();
 }

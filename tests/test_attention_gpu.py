@@ -111,6 +111,25 @@ def test_rope_on_load_matches_oracle(gpu, tokens):
     check(f"rope T={tokens}", got, expected)
 
 
+@pytest.mark.parametrize("tokens", [60, 130, 801])
+def test_gated_rope_on_unaligned_packed_rows(gpu, tokens):
+    # RoPE on load with rows whose stride is not a multiple of 4 floats (q | k | v | gates |
+    # 6 zero columns: 585 per row): the element-wise load path of both attention kernels.
+    groups, heads = 2, 3
+    q, k, v = (W.normal_torch((groups, tokens, heads, 64), s, 1.0, device=gpu) for s in (5, 6, 7))
+    gates = W.normal_torch((groups, tokens, heads), 8, 2.0, device=gpu)
+    flat = lambda t: t.reshape(groups, tokens, heads * 64)
+    packed = torch.cat([flat(q), flat(k), flat(v), gates,
+                        torch.zeros((groups, tokens, 6), device=gpu)], dim=2)
+    assert packed.shape[2] % 4 != 0
+    table = W.axis_rope_packed(W.rope_freqs(), tokens)
+    got = fused.gated_attention(packed, heads, rope=dev(table, gpu))
+    assert got is not None
+    expected = O.attention_op(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), rope=table)
+    expected = expected / (1.0 + np.exp(-gates.cpu().numpy().astype(np.float64)))[..., None]
+    check(f"gated rope unaligned T={tokens}", got.cpu().numpy(), expected)
+
+
 def test_rope_on_load_equals_prerotated_inputs(gpu):
     # The two boundary modes agree: rotation in the kernel vs q/k rotated (and q scaled) by
     # the caller, as the reference's GEMM epilogue does.
