@@ -108,23 +108,50 @@ __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitPara
   }
 }
 
-__global__ void glu_gather_kernel(GluParams p) {
-  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  const long total = (long)p.outputs * p.frames;
-  if (idx >= total) return;
-  const int t = (int)(idx % p.frames), o = (int)(idx / p.frames);
-  const int f = o >> 2, within = o & 3;  // column 2*channel + re/im of bin f
-  const int e0 = p.cover_start[f], e1 = p.cover_start[f + 1];
-  float sum = 0.0f;
-  for (int e = e0; e < e1; e++) {
-    const int b = p.cover_band[e], col = 4 * p.cover_local[e] + within;
-    const float* row = p.glu + p.band_base[b] * p.frames + (long)t * p.band_stride[b];
-    const float value = row[col], gate = row[p.band_width[b] + col];
-    sum += value * (1.0f / (1.0f + expf(-gate)));
+// One workgroup per tile of 64 outputs x 64 frames. Lanes run along the outputs, so a wave
+// reads consecutive columns of one band row (the rows are frame-major); the tile is transposed
+// through LDS and written frame-contiguous, each wave storing whole 256-byte rows.
+constexpr int kGluTile = 64;
+__global__ __launch_bounds__(256) void glu_gather_kernel(GluParams p) {
+  __shared__ float tile[kGluTile][kGluTile + 1];
+  const int o0 = blockIdx.x * kGluTile, t0 = blockIdx.y * kGluTile;
+  const int lane = threadIdx.x & 63, sub = threadIdx.x >> 6;
+  const int o = o0 + lane;
+  if (o < p.outputs) {
+    const int f = o >> 2, within = o & 3;  // column 2*channel + re/im of bin f
+    const int e0 = p.cover_start[f], e1 = p.cover_start[f + 1];
+    const int nt = min(kGluTile / 4, (p.frames - t0 - sub + 3) / 4);  // frames t0 + sub + 4 i
+    float sum[kGluTile / 4];
+#pragma unroll
+    for (int i = 0; i < kGluTile / 4; i++) sum[i] = 0.0f;
+    // Covering bands in order (the summation order of the reference), each band's row pointer
+    // and gate offset read once for the tile's 16 frames of this thread.
+    for (int e = e0; e < e1; e++) {
+      const int b = p.cover_band[e], col = 4 * p.cover_local[e] + within;
+      const long stride = p.band_stride[b];
+      const float* row = p.glu + p.band_base[b] * p.frames + (long)(t0 + sub) * stride + col;
+      const int gate = p.band_width[b];
+#pragma unroll
+      for (int i = 0; i < kGluTile / 4; i++)
+        if (i < nt) {
+          const float* r = row + (long)(4 * i) * stride;
+          sum[i] += r[0] * (1.0f / (1.0f + expf(-r[gate])));
+        }
+    }
+    const float count = (float)(e1 - e0);
+#pragma unroll
+    for (int i = 0; i < kGluTile / 4; i++)
+      if (i < nt) {
+        const float mask = sum[i] / count;
+        if (p.flags && non_finite(mask)) raise_flag(p.flags, kFlagMasks);
+        tile[lane][sub + 4 * i] = mask;
+      }
   }
-  const float mask = sum / (float)(e1 - e0);
-  if (p.flags && non_finite(mask)) raise_flag(p.flags, kFlagMasks);
-  p.masks[(long)o * p.frames + t] = mask;
+  __syncthreads();
+  for (int r = sub; r < kGluTile; r += 4) {
+    const int oo = o0 + r, t = t0 + lane;
+    if (oo < p.outputs && t < p.frames) p.masks[(long)oo * p.frames + t] = tile[r][lane];
+  }
 }
 
 }  // namespace
@@ -139,9 +166,8 @@ hipError_t launch_band_split(const BandSplitParams& params, hipStream_t stream) 
 }
 
 hipError_t launch_glu_gather(const GluParams& p, hipStream_t stream) {
-  const long total = (long)p.outputs * p.frames;
-  hipLaunchKernelGGL(glu_gather_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0,
-                     stream, p);
+  const dim3 grid((p.outputs + kGluTile - 1) / kGluTile, (p.frames + kGluTile - 1) / kGluTile);
+  hipLaunchKernelGGL(glu_gather_kernel, grid, dim3(256), 0, stream, p);
   return hipGetLastError();
 }
 
