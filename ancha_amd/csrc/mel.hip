@@ -30,11 +30,14 @@ constexpr int kSplitJobs = 2 * 512 / kSplitDims;  // (channel group, frame half)
 // time, so a thread reads its 16 frames of a column as four 16-byte words and its 4 weights as
 // one: 64 FMAs per 5 loads. Squared norms accumulate over the passes; 1/norm is applied last.
 // 32 frames per workgroup amortise the gather of the band's spectrum columns (two dependent
-// global reads) over twice the arithmetic of a 16-frame tile.
+// global reads) over twice the arithmetic of a 16-frame tile; the workgroup has one thread per
+// job (192 at dim 384).
 __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitParams p) {
   __shared__ __attribute__((aligned(16))) float zt[kSplitCols * kSplitFrames];
   __shared__ float sq[kSplitFrames];
-  const int b = blockIdx.x, t0 = blockIdx.y * kSplitFrames;
+  // Bands run high to low: both band layouts list them by frequency, so the widest (the
+  // longest workgroups) are dispatched first and the narrow ones fill in behind them.
+  const int b = p.bands - 1 - (int)blockIdx.y, t0 = blockIdx.x * kSplitFrames;
   const int q0 = p.offsets[b], nb = p.offsets[b + 1] - q0, width = 4 * nb;
   const int frames = min(kSplitFrames, p.frames - t0);
   const float* w = p.weight + (long)p.wofs[b] * p.dim;
@@ -51,7 +54,7 @@ __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitPara
   for (int c0 = 0; c0 < width; c0 += kSplitCols) {
     const int cols = min(kSplitCols, width - c0), bins = cols / 4;
     __syncthreads();  // the previous pass is done with zt
-    for (int e = threadIdx.x; e < kSplitFrames * bins; e += kSplitThreads) {
+    for (int e = threadIdx.x; e < kSplitFrames * bins; e += blockDim.x) {
       const int tt = e % kSplitFrames, q = e / kSplitFrames;
       float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
       if (tt < frames)
@@ -64,7 +67,7 @@ __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitPara
     }
     __syncthreads();
     // squared norms: 16 lanes per frame
-    for (int tt = threadIdx.x >> 4; tt < kSplitFrames; tt += kSplitThreads / 16) {
+    for (int tt = threadIdx.x >> 4; tt < kSplitFrames; tt += blockDim.x / 16) {
       const int l = threadIdx.x & 15;
       float s = 0.0f;
       for (int c = l; c < cols; c += 16) s += zt[c * kSplitFrames + tt] * zt[c * kSplitFrames + tt];
@@ -74,9 +77,19 @@ __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitPara
     if (active) {
       const float* zc = zt + half * kSplitHalf;
       const float* wc = w + (long)c0 * p.dim + d0;
-#pragma unroll 8
-      for (int c = 0; c < cols; c++) {
-        const float4 wv = *reinterpret_cast<const float4*>(wc + (long)c * p.dim);
+      // Weight rows stream through a ring of kRing registers, kRing columns ahead of their FMAs.
+      constexpr int kRing = 8;
+      float4 ring[kRing];
+#pragma unroll
+      for (int u = 0; u < kRing; u++)
+        if (u < cols) ring[u] = *reinterpret_cast<const float4*>(wc + (long)u * p.dim);
+      for (int cb = 0; cb < cols; cb += kRing)
+#pragma unroll
+      for (int u = 0; u < kRing; u++) {
+        const int c = cb + u;
+        if (c >= cols) break;
+        const float4 wv = ring[u];
+        if (c + kRing < cols) ring[u] = *reinterpret_cast<const float4*>(wc + (long)(c + kRing) * p.dim);
         float zz[kSplitHalf];
 #pragma unroll
         for (int k = 0; k < kSplitHalf / 4; k++) {
@@ -160,8 +173,9 @@ hipError_t launch_band_split(const BandSplitParams& params, hipStream_t stream) 
   BandSplitParams p = params;
   if (p.dim % kSplitDims || 2 * p.dim / kSplitDims > kSplitJobs) return hipErrorInvalidValue;
   p.tile = kSplitFrames;
-  const dim3 grid(p.bands, (p.frames + kSplitFrames - 1) / kSplitFrames);
-  hipLaunchKernelGGL(band_split_kernel, grid, dim3(kSplitThreads), 0, stream, p);
+  const dim3 grid((p.frames + kSplitFrames - 1) / kSplitFrames, p.bands);
+  // One thread per (channel group, frame half) job: 192 threads at dim 384, 256 at 512.
+  hipLaunchKernelGGL(band_split_kernel, grid, dim3(2 * p.dim / kSplitDims), 0, stream, p);
   return hipGetLastError();
 }
 
