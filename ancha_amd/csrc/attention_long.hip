@@ -156,7 +156,33 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
   // Passes run in rounds of `grid`; odd rounds walk backwards, so a workgroup alternates between
   // the full and the partial query blocks of a (group, head) and both halves of one (group,
   // head) run side by side on neighbouring workgroups of one XCD (shared K / V in its L2).
+  //
+  // Two query blocks per (group, head) (T = 513 .. 1024) when the rounds do not come out even:
+  // the workgroups with one pass more than the others should get the cheap partial blocks. Each
+  // XCD's workgroups split into halves B and A; in every full round, B workgroup jj runs the full
+  // block and A workgroup jj the partial block of one (group, head), side by side as above; the
+  // leftover (group, head) problems then run on A workgroups only, two neighbours per problem.
+  // B ends with full rounds only, A with one pass more, most of them partial (at T = 801 and 960
+  // problems on 256 CUs: A 7 partial + 1 against 4 full + 4 partial for the alternating walk).
+  // When the rounds come out even the alternating walk is the balanced one and stays.
+  const int xcd_wgs = grid / kXcds, pair_half = xcd_wgs / 2, pairs = grid / 2;
+  const int problems = passes / 2, full_rounds = qblocks == 2 ? problems / pairs : 0;
+  const int leftover = problems - full_rounds * pairs;
+  const bool paired = qblocks == 2 && grid % (2 * kXcds) == 0 && passes > 2 * grid &&
+                      leftover > 0 && 2 * leftover <= pairs;
+  const int px = lb / (xcd_wgs > 0 ? xcd_wgs : 1), pj = lb % (xcd_wgs > 0 ? xcd_wgs : 1);
+  const bool pa = pj >= pair_half;
+  const int pjj = pa ? pj - pair_half : pj;
   auto pass_of = [&](int rnd) -> long {
+    if (paired) {
+      if (rnd < full_rounds) {
+        const long problem = ((long)rnd * kXcds + px) * pair_half + pjj;
+        return 2 * problem + (pa ? 1 : 0);
+      }
+      const int idx = px * pair_half + pjj;
+      if (rnd > full_rounds || !pa || idx >= 2 * leftover) return passes;
+      return 2 * ((long)full_rounds * pairs + idx / 2) + (idx & 1);
+    }
     return (long)rnd * grid + ((rnd & 1) ? grid - 1 - lb : lb);
   };
   // Per-pass opaque copies (set at the top of every pass): the compiler cannot hoist values

@@ -91,13 +91,15 @@ __device__ __forceinline__ int xcd_remap(int b, int n) {
 }
 
 // Interleaved-pair rotation of 4 consecutive channels (two pairs):
-// y = x*cos + swap_pairs(x)*sin, the pair sign folded into sin.
+// y = x*cos + swap_pairs(x)*sin, the pair sign folded into sin. The fused multiply-add is
+// written out, so every call site rounds the same way (left to the compiler, the contraction of
+// the two products can differ between inlined copies and move a rotated value by one ulp).
 __device__ __forceinline__ float4 rotate4(float4 x, float4 c, float4 s) {
   float4 y;
-  y.x = x.x * c.x + x.y * s.x;
-  y.y = x.y * c.y + x.x * s.y;
-  y.z = x.z * c.z + x.w * s.z;
-  y.w = x.w * c.w + x.z * s.w;
+  y.x = __builtin_fmaf(x.x, c.x, x.y * s.x);
+  y.y = __builtin_fmaf(x.y, c.y, x.x * s.y);
+  y.z = __builtin_fmaf(x.z, c.z, x.w * s.z);
+  y.w = __builtin_fmaf(x.w, c.w, x.z * s.w);
   return y;
 }
 
