@@ -163,6 +163,12 @@ def test_time_axis_full_size(gpu):
     groups = [0, 61, 119]
     expected = oracle_slice(q, k, v, table, groups)
     check("time full-size", out[groups].cpu().numpy(), expected)
+    # Every (group, head) pass, against the fp32 restatement: the persistent walk (here the
+    # paired walk of uneven rounds) must cover each pass exactly once.
+    ref = torch_attention(q, k, v, dev(table, gpu))
+    err = float((out - ref).abs().max())
+    print(f"time full-size, all groups vs fp32: max|diff| {err:.3e}", flush=True)
+    assert err <= REL * float(ref.abs().max())
     again = fused.attention(q, k, v, rope=dev(table, gpu))
     assert torch.equal(out, again), "kernel must be deterministic"
 
