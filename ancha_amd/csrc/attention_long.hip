@@ -160,10 +160,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
   // Two query blocks per (group, head) (T = 513 .. 1024) when the rounds do not come out even:
   // the workgroups with one pass more than the others should get the cheap partial blocks. Each
   // XCD's workgroups split into halves B and A; in every full round, B workgroup jj runs the full
-  // block and A workgroup jj the partial block of one (group, head), side by side as above; the
+  // block and A workgroup jj the partial block of one (group, head) of the same XCD; the
   // leftover (group, head) problems then run on A workgroups only, two neighbours per problem.
   // B ends with full rounds only, A with one pass more, most of them partial (at T = 801 and 960
   // problems on 256 CUs: A 7 partial + 1 against 4 full + 4 partial for the alternating walk).
+  // The partial side gains ~7 % of a pass per round on its partner, so after the first rounds
+  // the two reads of a K / V stream no longer meet in L2: the balance is worth more here.
   // When the rounds come out even the alternating walk is the balanced one and stays.
   const int xcd_wgs = grid / kXcds, pair_half = xcd_wgs / 2, pairs = grid / 2;
   const int problems = passes / 2, full_rounds = qblocks == 2 ? problems / pairs : 0;
