@@ -395,24 +395,32 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
     o[0] = zero16();
     o[1] = zero16();
     float negm = 0.f, lsum = 0.f;  // -(running maximum), this lane's share of the row sum
+    // The running maximum starts at the exact maximum over the first 32 keys (T > 64); their
+    // scores are kept for the first block, which then needs no score MFMAs of its own.
+    f32x16 s0 = zero16();
     if (active) {
-      // The running maximum starts at the exact maximum over the first 32 keys (T > 64).
-      f32x16 s = zero16();
 #pragma unroll
-      for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(lds_k[buf] + fq[ds]), qf[ds], s);
-      float mx = fmaxf(fmaxf(s[0], s[1]), s[2]);
+      for (int ds = 0; ds < 4; ds++) s0 = mfma32(lds16(lds_k[buf] + fq[ds]), qf[ds], s0);
+      float mx = fmaxf(fmaxf(s0[0], s0[1]), s0[2]);
 #pragma unroll
-      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s[r]), s[r + 1]);
-      negm = -pair_max(fmaxf(mx, s[15]));
+      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s0[r]), s0[r + 1]);
+      negm = -pair_max(fmaxf(mx, s0[15]));
     }
 
     // One 32-key block kb of the tile in buffer b. MASK: keys at or past T may be present.
-    auto block = [&](auto mask_tag, int b, int kb, int key0) {
+    // FIRST: the pass's first block, whose scores s0 are already computed (shifted here).
+    auto block = [&](auto mask_tag, int b, int kb, int key0, auto first_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
+      constexpr bool FIRST = decltype(first_tag)::value;
       const unsigned char* K = lds_k[b] + kb * 4096;
-      f32x16 s = seed16(negm);
+      f32x16 s;
+      if constexpr (FIRST) {
+        s = s0 + negm;
+      } else {
+        s = seed16(negm);
 #pragma unroll
-      for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(K + fq[ds]), qf[ds], s);
+        for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(K + fq[ds]), qf[ds], s);
+      }
       if constexpr (MASK) {
 #pragma unroll
         for (int i = 0; i < 4; i++)
@@ -458,10 +466,15 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
       // block, so that the 16 waves' loads do not all queue at the start of the step.
       load_tile(kbase, vbase, (j + 1) * 64, 1);
       const int c = j - cstart;
-      if (active) block(std::false_type{}, buf, 0, j * 64);
+      if (active) {
+        if (j == 0)
+          block(std::false_type{}, buf, 0, 0, std::true_type{});
+        else
+          block(std::false_type{}, buf, 0, j * 64, std::false_type{});
+      }
       load_tile(kbase, vbase, (j + 1) * 64, 2);
       if (prefetch && c >= 0) issue_chunk(row0n, hn, q0n, c);
-      if (active) block(std::false_type{}, buf, 1, j * 64);
+      if (active) block(std::false_type{}, buf, 1, j * 64, std::false_type{});
       __builtin_amdgcn_s_waitcnt(kWaitVmem);
       if (prefetch && c >= 0) convert_chunk(c);
       store_tile(buf ^ 1);
@@ -473,8 +486,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
     // next pass's first tile loads after its blocks, beside this pass's epilogue.
     if (active) {
       const int j = ntiles - 1;
-      block(std::true_type{}, buf, 0, j * 64);
-      block(std::true_type{}, buf, 1, j * 64);
+      block(std::true_type{}, buf, 0, j * 64, std::false_type{});
+      block(std::true_type{}, buf, 1, j * 64, std::false_type{});
     }
     if (has_next)
       load_tile(reinterpret_cast<const unsigned char*>(p.k) + (row0n * p.ldk + hn * 64) * kEsz,
