@@ -28,8 +28,9 @@ __device__ __forceinline__ float gelu_erf(float x) {
 // reciprocal. GELU(x) = x - x/2 erfc(x/sqrt2) for x >= 0 and x/2 erfc(-x/sqrt2) below, so the
 // negative tail keeps its relative accuracy.
 // The constants are folded for the VALU: p / sqrt2 multiplies |x| directly, the polynomial
-// carries the factor 1/2 (so h = x erfc(|x|/sqrt2) / 2 is three multiplies), and
-// exp(-z^2) = exp2(x^2 * (-log2(e) / 2)).
+// carries the factor 1/2 (so q = erfc(|x|/sqrt2) / 2 is two multiplies), and
+// exp(-z^2) = exp2(x^2 * (-log2(e) / 2)). Both branches are max(x, 0) - |x| q: x - x q for
+// x >= 0, x q below; one fused multiply-add with the sign and magnitude as operand modifiers.
 __device__ __forceinline__ float gelu_fast(float x) {
   const float t = __builtin_amdgcn_rcpf(fmaf(0.3275911f * 0.70710678118654752f, fabsf(x), 1.0f));
   float poly = fmaf(t, 0.5f * 1.061405429f, 0.5f * -1.453152027f);
@@ -37,8 +38,7 @@ __device__ __forceinline__ float gelu_fast(float x) {
   poly = fmaf(t, poly, 0.5f * -0.284496736f);
   poly = fmaf(t, poly, 0.5f * 0.254829592f);
   const float e = __builtin_amdgcn_exp2f(x * -0.72134752044448170f * x);
-  const float h = x * (poly * t * e);
-  return x >= 0.0f ? x - h : h;
+  return fmaf(-fabsf(x), poly * t * e, fmaxf(x, 0.0f));
 }
 
 // tanh as 1 - 2 / (e^{2|x|} + 1) with the sign restored; below |x| = 2^-8 the series

@@ -200,8 +200,23 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
 
     // ---- feed-forward, 128 hidden units per chunk.
     for (int c = 0; c < chunks; c++) {
-      // FF in: this wave's 32 hidden units 128 c + 32 fq + (8 q + 4 h + e).
-      f32x16 hacc[2] = {mfma32_zero(), mfma32_zero()};
+      // FF in: this wave's 32 hidden units 128 c + 32 fq + (8 q + 4 h + e), the accumulators
+      // starting at b1 (issued ahead of the chunk's first weight fragments, which the first MFMA
+      // waits for anyway).
+      f32x16 hacc[2];
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const float4 b = __builtin_bit_cast(
+            float4, __builtin_amdgcn_raw_buffer_load_b128(
+                        b1r, 16 * half, (unsigned)(kChunk * c + 32 * fq + 8 * q) * 4, 0));
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+          hacc[j][4 * q] = b.x;
+          hacc[j][4 * q + 1] = b.y;
+          hacc[j][4 * q + 2] = b.z;
+          hacc[j][4 * q + 3] = b.w;
+        }
+      }
       {
         constexpr int PD = 8;
         const int blk1 = 4 * c + fq;
@@ -231,23 +246,12 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
         }
       }
       // GELU(h + b1), fp16, into H as FF-out B fragments (hidden steps 2 fq, 2 fq + 1).
-      float4 bias[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        bias[q] = __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(
-                        b1r, 16 * half, (unsigned)(kChunk * c + 32 * fq + 8 * q) * 4, 0));
       __syncthreads();  // the previous chunk's FF-out has read H
 #pragma unroll
       for (int j = 0; j < 2; j++) {
         f32x16 g;
 #pragma unroll
-        for (int q = 0; q < 4; q++) {
-          g[4 * q] = gemm::gelu_fast(hacc[j][4 * q] + bias[q].x);
-          g[4 * q + 1] = gemm::gelu_fast(hacc[j][4 * q + 1] + bias[q].y);
-          g[4 * q + 2] = gemm::gelu_fast(hacc[j][4 * q + 2] + bias[q].z);
-          g[4 * q + 3] = gemm::gelu_fast(hacc[j][4 * q + 3] + bias[q].w);
-        }
+        for (int r = 0; r < 16; r++) g[r] = gemm::gelu_fast(hacc[j][r]);
 #pragma unroll
         for (int sub = 0; sub < 2; sub++)
           *reinterpret_cast<u32x4*>(H + ((2 * rh + j) * 8 + 2 * fq + sub) * kFrag + lane16) =
