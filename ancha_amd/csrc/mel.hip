@@ -83,27 +83,29 @@ __global__ __launch_bounds__(kSplitThreads) void band_split_kernel(BandSplitPara
 #pragma unroll
       for (int u = 0; u < kRing; u++)
         if (u < cols) ring[u] = *reinterpret_cast<const float4*>(wc + (long)u * p.dim);
-      for (int cb = 0; cb < cols; cb += kRing)
+      for (int cb = 0; cb < cols; cb += kRing) {
 #pragma unroll
-      for (int u = 0; u < kRing; u++) {
-        const int c = cb + u;
-        if (c >= cols) break;
-        const float4 wv = ring[u];
-        if (c + kRing < cols) ring[u] = *reinterpret_cast<const float4*>(wc + (long)(c + kRing) * p.dim);
-        float zz[kSplitHalf];
+        for (int u = 0; u < kRing; u++) {
+          const int c = cb + u;
+          if (c >= cols) break;
+          const float4 wv = ring[u];
+          if (c + kRing < cols)
+            ring[u] = *reinterpret_cast<const float4*>(wc + (long)(c + kRing) * p.dim);
+          float zz[kSplitHalf];
 #pragma unroll
-        for (int k = 0; k < kSplitHalf / 4; k++) {
-          const float4 z = *reinterpret_cast<const float4*>(zc + c * kSplitFrames + 4 * k);
-          zz[4 * k] = z.x;
-          zz[4 * k + 1] = z.y;
-          zz[4 * k + 2] = z.z;
-          zz[4 * k + 3] = z.w;
+          for (int k = 0; k < kSplitHalf / 4; k++) {
+            const float4 z = *reinterpret_cast<const float4*>(zc + c * kSplitFrames + 4 * k);
+            zz[4 * k] = z.x;
+            zz[4 * k + 1] = z.y;
+            zz[4 * k + 2] = z.z;
+            zz[4 * k + 3] = z.w;
+          }
+          const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+          for (int i = 0; i < kSplitHalf; i++)
+#pragma unroll
+            for (int j = 0; j < kSplitDims; j++) acc[i][j] += ww[j] * zz[i];
         }
-        const float ww[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-        for (int i = 0; i < kSplitHalf; i++)
-#pragma unroll
-          for (int j = 0; j < kSplitDims; j++) acc[i][j] += ww[j] * zz[i];
       }
     }
   }
