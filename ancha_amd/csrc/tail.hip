@@ -23,8 +23,9 @@
 // Workgroup: 64 rows, 4 waves, one per feature quarter (and SIMD); two workgroups per CU, whose
 // phases drift apart, so one's GELU / norm VALU work runs beside the other's MFMAs. The out
 // accumulator (64 rows x dim) stays in registers from the residual load to the final store; the
-// hidden dimension runs in chunks of 128 (per chunk: FF-in for 32 hidden units per wave, GELU,
-// the chunk's fp16 activation to LDS, then its FF-out contribution).
+// hidden dimension runs in chunks of 256 units up to dim 384, 128 at dim 512 (per chunk: FF-in
+// for 64 or 32 hidden units per wave, GELU, the chunk's fp16 activation to LDS, then its FF-out
+// contribution).
 #include "buffer.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
@@ -35,7 +36,7 @@ namespace {
 
 
 constexpr int kRows = 64;         // rows per workgroup step
-constexpr int kChunk = 128;       // hidden units per chunk
+constexpr int kChunk = 128;       // hidden units of one 32-unit block per wave (4 waves)
 constexpr int kWaves = 4;         // one per feature quarter (and per SIMD)
 constexpr int kFrag = 1024;       // bytes of one 32 x 16 fp16 fragment
 // B fragments are read from LDS this many k steps ahead of their MFMAs (a scheduling barrier
@@ -73,12 +74,17 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
   constexpr int S0 = INNER / 16;   // k steps of the out projection
   constexpr int SD = DIM / 16;     // k steps of FF in
   constexpr int kX = kRows * DIM * 2;                                   // xh1 fragments
-  constexpr int kLds = (kRows * INNER * 2 > kX + kRows * kChunk * 2) ? kRows * INNER * 2
-                                                                      : kX + kRows * kChunk * 2;
+  // Hidden blocks of 32 units per wave and chunk: two where the chunk's activation (32 KB) still
+  // leaves two workgroups a CU (dim <= 384), so each X fragment feeds two MFMAs of FF in.
+  constexpr int NB = NI <= 3 ? 2 : 1;
+  constexpr int kCH = kChunk * NB;  // hidden units per chunk
+  constexpr int kSC = kCH / 16;     // k steps of FF out per chunk
+  constexpr int kLds = (kRows * INNER * 2 > kX + kRows * kCH * 2) ? kRows * INNER * 2
+                                                                   : kX + kRows * kCH * 2;
   static_assert(kLds <= 160 * 1024, "LDS");
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLds];
   unsigned char* const X = lds;         // xh1: fragment (jb, s) at (jb * SD + s) * 1 KB
-  unsigned char* const H = lds + kX;    // hidden chunk: fragment (jb, s) at (jb * 8 + s) * 1 KB
+  unsigned char* const H = lds + kX;    // hidden chunk: fragment (jb, s) at (jb * kSC + s) * 1 KB
   float* const red = reinterpret_cast<float*>(H);  // [4][128] row partials (aliases H)
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -86,7 +92,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
   constexpr int rh = 0;  // the workgroup's 64 rows are one pair of 32-row blocks
   const int fq = wave;
   const int half = lane >> 5, col = lane & 31;
-  const int hidden = p.hidden, chunks = hidden / kChunk;
+  const int hidden = p.hidden;
   const unsigned lane16 = (unsigned)lane * 16;
 
   const rsrc_t wo = make_rsrc(p.wo, (unsigned)(DIM * INNER * 2));
@@ -198,33 +204,39 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
     }
     __syncthreads();
 
-    // ---- feed-forward, 128 hidden units per chunk.
-    for (int c = 0; c < chunks; c++) {
-      // FF in: this wave's 32 hidden units 128 c + 32 fq + (8 q + 4 h + e), the accumulators
-      // starting at b1 (issued ahead of the chunk's first weight fragments, which the first MFMA
-      // waits for anyway).
-      f32x16 hacc[2];
+    // ---- feed-forward, NB x 128 hidden units per chunk (NB 32-unit hidden blocks per wave).
+    for (int c = 0; c < hidden / kCH; c++) {
+      // FF in: this wave's hidden blocks NB fq + x (x < NB) of the chunk, units kCH c +
+      // 32 (NB fq + x) + (8 q + 4 h + e), the accumulators starting at b1 (issued ahead of the
+      // chunk's first weight fragments, which the first MFMA waits for anyway).
+      f32x16 hacc[NB][2];
 #pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const float4 b = __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(
-                        b1r, 16 * half, (unsigned)(kChunk * c + 32 * fq + 8 * q) * 4, 0));
+      for (int x = 0; x < NB; x++)
 #pragma unroll
-        for (int j = 0; j < 2; j++) {
-          hacc[j][4 * q] = b.x;
-          hacc[j][4 * q + 1] = b.y;
-          hacc[j][4 * q + 2] = b.z;
-          hacc[j][4 * q + 3] = b.w;
+        for (int q = 0; q < 4; q++) {
+          const float4 b = __builtin_bit_cast(
+              float4, __builtin_amdgcn_raw_buffer_load_b128(
+                          b1r, 16 * half, (unsigned)(kCH * c + 32 * (NB * fq + x) + 8 * q) * 4, 0));
+#pragma unroll
+          for (int j = 0; j < 2; j++) {
+            hacc[x][j][4 * q] = b.x;
+            hacc[x][j][4 * q + 1] = b.y;
+            hacc[x][j][4 * q + 2] = b.z;
+            hacc[x][j][4 * q + 3] = b.w;
+          }
         }
-      }
       {
-        constexpr int PD = 8;
-        const int blk1 = 4 * c + fq;
-        u32x4 a[PD];
+        constexpr int PD = NB > 1 ? 4 : 8;
+        const int blk0 = (kCH / 32) * c + NB * fq;
+        u32x4 a[PD][NB];
+        auto load_a = [&](int s, u32x4 (&dst)[NB]) {
 #pragma unroll
-        for (int s = 0; s < PD && s < SD; s++)
-          a[s] = __builtin_amdgcn_raw_buffer_load_b128(w1, lane16,
-                                                       (unsigned)((blk1 * SD + s) * kFrag), 0);
+          for (int x = 0; x < NB; x++)
+            dst[x] = __builtin_amdgcn_raw_buffer_load_b128(
+                w1, lane16, (unsigned)(((blk0 + x) * SD + s) * kFrag), 0);
+        };
+#pragma unroll
+        for (int s = 0; s < PD && s < SD; s++) load_a(s, a[s]);
         u32x4 b[kBD + 1][2];
         auto load_b = [&](int s, u32x4 (&dst)[2]) {
 #pragma unroll
@@ -235,30 +247,35 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
         for (int s = 0; s < kBD; s++) load_b(s, b[s]);
 #pragma unroll
         for (int s = 0; s < SD; s++) {
-          const u32x4 cur = a[s % PD];
-          if (s + PD < SD)
-            a[s % PD] = __builtin_amdgcn_raw_buffer_load_b128(
-                w1, lane16, (unsigned)((blk1 * SD + s + PD) * kFrag), 0);
+          u32x4 cur[NB];
+#pragma unroll
+          for (int x = 0; x < NB; x++) cur[x] = a[s % PD][x];
+          if (s + PD < SD) load_a(s + PD, a[s % PD]);
           if (s + kBD < SD) load_b(s + kBD, b[(s + kBD) % (kBD + 1)]);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-          for (int j = 0; j < 2; j++) hacc[j] = mfma32(cur, b[s % (kBD + 1)][j], hacc[j]);
+          for (int x = 0; x < NB; x++)
+#pragma unroll
+            for (int j = 0; j < 2; j++)
+              hacc[x][j] = mfma32(cur[x], b[s % (kBD + 1)][j], hacc[x][j]);
         }
       }
-      // GELU(h + b1), fp16, into H as FF-out B fragments (hidden steps 2 fq, 2 fq + 1).
+      // GELU(h + b1), fp16, into H as FF-out B fragments (hidden steps 2 (NB fq + x) + sub).
       __syncthreads();  // the previous chunk's FF-out has read H
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        f32x16 g;
+      for (int x = 0; x < NB; x++)
 #pragma unroll
-        for (int r = 0; r < 16; r++) g[r] = gemm::gelu_fast(hacc[j][r]);
+        for (int j = 0; j < 2; j++) {
+          f32x16 g;
 #pragma unroll
-        for (int sub = 0; sub < 2; sub++)
-          *reinterpret_cast<u32x4*>(H + ((2 * rh + j) * 8 + 2 * fq + sub) * kFrag + lane16) =
-              pack_frag(g, sub, 1.0f);
-      }
+          for (int r = 0; r < 16; r++) g[r] = gemm::gelu_fast(hacc[x][j][r]);
+#pragma unroll
+          for (int sub = 0; sub < 2; sub++)
+            *reinterpret_cast<u32x4*>(H + ((2 * rh + j) * kSC + 2 * (NB * fq + x) + sub) * kFrag +
+                                      lane16) = pack_frag(g, sub, 1.0f);
+        }
       __syncthreads();
-      // FF out: acc += W2^T . h^T over the chunk's 128 hidden units (8 steps of 16).
+      // FF out: acc += W2^T . h^T over the chunk's kCH hidden units (kSC steps of 16).
       {
         constexpr int PD = NI > 3 ? 2 : 4;
         const int sh = hidden / 16;
@@ -267,7 +284,7 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
 #pragma unroll
           for (int i = 0; i < NI; i++)
             dst[i] = __builtin_amdgcn_raw_buffer_load_b128(
-                w2, lane16, (unsigned)(((fq * NI + i) * sh + 8 * c + s) * kFrag), 0);
+                w2, lane16, (unsigned)(((fq * NI + i) * sh + kSC * c + s) * kFrag), 0);
         };
 #pragma unroll
         for (int s = 0; s < PD; s++) load_a(s, a[s]);
@@ -275,17 +292,17 @@ __global__ __launch_bounds__(kWaves * 64, 2) void block_tail_kernel(TailParams p
         auto load_b = [&](int s, u32x4 (&dst)[2]) {
 #pragma unroll
           for (int j = 0; j < 2; j++)
-            dst[j] = *reinterpret_cast<const u32x4*>(H + ((2 * rh + j) * 8 + s) * kFrag + lane16);
+            dst[j] = *reinterpret_cast<const u32x4*>(H + ((2 * rh + j) * kSC + s) * kFrag + lane16);
         };
 #pragma unroll
         for (int s = 0; s < kBD; s++) load_b(s, b[s]);
 #pragma unroll
-        for (int s = 0; s < 8; s++) {
+        for (int s = 0; s < kSC; s++) {
           u32x4 cur[NI];
 #pragma unroll
           for (int i = 0; i < NI; i++) cur[i] = a[s % PD][i];
-          if (s + PD < 8) load_a(s + PD, a[s % PD]);
-          if (s + kBD < 8) load_b(s + kBD, b[(s + kBD) % (kBD + 1)]);
+          if (s + PD < kSC) load_a(s + PD, a[s % PD]);
+          if (s + kBD < kSC) load_b(s + kBD, b[(s + kBD) % (kBD + 1)]);
           __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int i = 0; i < NI; i++)
@@ -395,8 +412,10 @@ hipError_t launch_t(const TailParams& p, int grid, hipStream_t stream) {
 }  // namespace
 
 bool block_tail_supported(int dim, int inner, int hidden) {
+  // Chunks of 256 hidden units up to dim 384, of 128 at dim 512.
+  const int chunk = dim <= 384 ? 2 * kChunk : kChunk;
   return (dim == 128 || dim == 256 || dim == 384 || dim == 512) && (inner == 128 || inner == 512) &&
-         hidden > 0 && hidden % kChunk == 0;
+         hidden > 0 && hidden % chunk == 0;
 }
 
 hipError_t launch_block_tail(const TailParams& p, hipStream_t stream) {
