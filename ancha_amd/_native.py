@@ -54,6 +54,7 @@ SIGNATURES = {
     "ancha_hip_roformer_create": (_int, [_p, _p, _p, ctypes.POINTER(_p)]),
     "ancha_hip_roformer_workspace": (_sz, [_p, _sz]),
     "ancha_hip_roformer_forward": (_int, [_p, _p, _sz, _p, _sz, _p, _p, _p]),
+    "ancha_hip_chunk_plan": (_int, [_sz, _sz, _sz, ctypes.POINTER(_sz), ctypes.POINTER(_sz)]),
     "ancha_hip_separate_workspace": (_sz, [_p, _sz]),
     "ancha_hip_separate": (_int, [_p, _p, _sz, _p, _sz, _p, _p, _p, _p]),
     "ancha_hip_roformer_destroy": (None, [_p]),

@@ -6,7 +6,9 @@
 #include <atomic>
 #include <cstdint>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "../../include/ancha_hip.h"
@@ -16,7 +18,33 @@
 namespace {
 
 std::atomic<int> g_sticky{0};
+// Text of the failure that set g_sticky (written once, by the call that set it).
+std::mutex g_first_mu;
+std::string g_first;
 thread_local std::string g_last;
+
+// Records the first failure of the process: `code` becomes the sticky state and `text` the
+// description every later call reports (device::record keeps the first panic message,
+// src/device.rs:11-28).
+int record_failure(int code, const std::string& text) {
+  std::lock_guard<std::mutex> lock(g_first_mu);
+  int expected = 0;
+  if (g_sticky.compare_exchange_strong(expected, code)) g_first = text;
+  return code;
+}
+
+// Failure injection for the tests of the sticky contract: ANCHA_HIP_INJECT_FAILURE=<positive
+// hipError_t code> in the environment when the library loads starts the process in the failed
+// state that HIP error would have left (tests/device_guard.rs of the reference drives its guard
+// the same way, from the host). Nothing else reads the variable.
+[[maybe_unused]] const int g_injected = [] {
+  const char* v = std::getenv("ANCHA_HIP_INJECT_FAILURE");
+  const int code = v ? std::atoi(v) : 0;
+  if (code > 0)
+    record_failure(-code, "injected failure (ANCHA_HIP_INJECT_FAILURE=" + std::to_string(code) +
+                              ")");
+  return code;
+}();
 
 }  // namespace
 
@@ -28,16 +56,19 @@ int fail(int code, const std::string& msg) {
 }
 
 int hip_fail(hipError_t e, const std::string& where) {
-  const int code = -static_cast<int>(e);
-  int expected = 0;
-  g_sticky.compare_exchange_strong(expected, code);
-  g_last = where + ": " + hipGetErrorString(e);
-  return code;
+  const std::string text = where + ": " + hipGetErrorString(e);
+  record_failure(-static_cast<int>(e), text);
+  g_last = text;
+  return -static_cast<int>(e);
 }
 
 int sticky() {
   const int s = g_sticky.load();
-  if (s) g_last = "an earlier HIP call failed (sticky device failure " + std::to_string(s) + ")";
+  if (s) {
+    std::lock_guard<std::mutex> lock(g_first_mu);
+    g_last = "an earlier HIP call failed (sticky device failure " + std::to_string(s) +
+             "): " + g_first;
+  }
   return s;
 }
 

@@ -139,7 +139,6 @@ __global__ void ola_accumulate_kernel(const float* frames_buf, int frames, int h
   const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= length) return;
   const long pos = start + i;
-  if (pos >= total) return;
   const long j = i + kN / 2;
   long t0 = j - kN + 1 > 0 ? (j - kN + 1 + hop - 1) / hop : 0;
   long t1 = j / hop;
@@ -152,15 +151,18 @@ __global__ void ola_accumulate_kernel(const float* frames_buf, int frames, int h
     a1 += frames_buf[t * 2 * kN + kN + o];
     den += w * w;
   }
-  const long fade = length / 10 > 1 ? length / 10 : 1;
-  float wt = 1.0f;
-  if (!first && i < fade) wt = (float)(i + 1) / (float)fade;
-  if (!last && i >= length - fade) wt = (float)(length - i) / (float)fade;
   const float y0 = a0 / den, y1 = a1 / den;
+  // Every sample of the chunk is checked, also those past the clip's end, which are not
+  // accumulated (Stft::inverse and Accumulator::add check whole planes).
   if (flags) {
     if (!(den > 1e-11f)) raise_flag(flags, kFlagIstftUncovered);
     if (non_finite(y0) || non_finite(y1)) raise_flag(flags, kFlagChunk);
   }
+  if (pos >= total) return;
+  const long fade = length / 10 > 1 ? length / 10 : 1;
+  float wt = 1.0f;
+  if (!first && i < fade) wt = (float)(i + 1) / (float)fade;
+  if (!last && i >= length - fade) wt = (float)(length - i) / (float)fade;
   sums[pos] += wt * y0;
   sums[total + pos] += wt * y1;
   if (count_weight) weights[pos] += wt;
@@ -189,10 +191,14 @@ __global__ void chunk_gather_kernel(const float* audio, long n, long start, long
 __global__ void finish_kernel(const float* sums, const float* weights, long total, long border,
                               long n, const float* audio, float* out, float* residual,
                               unsigned* flags) {
-  const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const float w = weights[border + i];
+  // One thread per accumulator sample: every weight is checked (Accumulator::finish), the
+  // samples of the cropped clip [border, border + n) are written.
+  const long idx = (long)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const float w = weights[idx];
   if (flags && !(w > 0.0f)) raise_flag(flags, kFlagOlaUncovered);
+  const long i = idx - border;
+  if (i < 0 || i >= n) return;
   for (int c = 0; c < 2; c++) {
     const float y = sums[c * total + border + i] / w;
     out[c * n + i] = y;
@@ -245,7 +251,7 @@ hipError_t launch_chunk_gather(const float* audio, long n, long start, long bord
 hipError_t launch_finish(const float* sums, const float* weights, long total, long border, long n,
                          const float* audio, float* out, float* residual, unsigned* flags,
                          hipStream_t stream) {
-  hipLaunchKernelGGL(finish_kernel, dim3(blocks_for(n, 256)), dim3(256), 0, stream, sums, weights,
+  hipLaunchKernelGGL(finish_kernel, dim3(blocks_for(total, 256)), dim3(256), 0, stream, sums, weights,
                      total, border, n, audio, out, residual, flags);
   return hipGetLastError();
 }

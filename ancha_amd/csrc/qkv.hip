@@ -180,7 +180,9 @@ bool qkv_supported(int dim, int cols) {
 }
 
 hipError_t launch_qkv(const QkvParams& p, hipStream_t stream) {
-  if (!qkv_supported(p.dim, p.cols) || (p.rope && (p.tokens <= 0 || p.token_div <= 0)))
+  // The query scaling rides on the rotary epilogue: a table is required (the block always
+  // passes one; without it the query columns would come out unscaled).
+  if (!qkv_supported(p.dim, p.cols) || !p.rope || p.tokens <= 0 || p.token_div <= 0)
     return hipErrorInvalidValue;
   if (p.rows <= 0) return hipSuccess;
   const int cus = device_cus();

@@ -323,18 +323,24 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
   return 0;
 }
 
-// Chunk plan of src/runtime.rs:103-116 and ChunkPlan (chunk.rs:1-25).
+// Chunk plan of src/runtime.rs:103-116 and ChunkPlan (chunk.rs:1-25): chunks start every
+// chunk / overlap samples over the clip plus a reflected border of chunk - step samples on
+// each side (no border when the clip is not longer than two borders).
 struct Plan {
   size_t step, border, length, frames;
   std::vector<size_t> starts;
 };
-Plan plan_for(const ancha_hip_roformer* m, size_t samples) {
+Plan plan_of(size_t chunk, size_t overlap, size_t samples) {
   Plan p{};
-  p.step = m->chunk / m->overlap;
-  p.border = m->chunk - p.step;
+  p.step = chunk / overlap;
+  p.border = chunk - p.step;
   if (!(samples > 2 * p.border)) p.border = 0;
   p.length = samples + 2 * p.border;
   for (size_t s = 0; s < p.length; s += p.step) p.starts.push_back(s);
+  return p;
+}
+Plan plan_for(const ancha_hip_roformer* m, size_t samples) {
+  Plan p = plan_of(m->chunk, m->overlap, samples);
   p.frames = m->chunk / m->hop + 1;
   return p;
 }
@@ -659,6 +665,20 @@ int ancha_hip_roformer_forward(ancha_hip_roformer* m, const float* spectrum, siz
   return forward_impl(m, &spectrum, 1, frames, workspace, &masks, cancelled, nullptr, stream);
 }
 
+int ancha_hip_chunk_plan(size_t chunk_samples, size_t overlap, size_t samples, size_t* chunks,
+                         size_t* border) {
+  if (chunk_samples == 0 || overlap == 0 || overlap > chunk_samples)
+    return ancha::fail(ANCHA_HIP_INVALID, "ancha_hip_chunk_plan: invalid chunk or overlap divisor");
+  if (samples > (size_t(1) << 40))
+    return ancha::fail(ANCHA_HIP_UNSUPPORTED, "ancha_hip_chunk_plan: clip too long");
+  const size_t step = chunk_samples / overlap;
+  const size_t b = 2 * (chunk_samples - step) < samples ? chunk_samples - step : 0;
+  // starts = 0, step, ... below samples + 2 * border: the count plan_of's loop produces.
+  if (chunks) *chunks = (samples + 2 * b + step - 1) / step;
+  if (border) *border = b;
+  return ANCHA_HIP_OK;
+}
+
 size_t ancha_hip_separate_workspace(const ancha_hip_roformer* m, size_t samples) {
   if (!m || samples == 0) return 0;
   return separate_layout(m, samples).total;
@@ -666,12 +686,17 @@ size_t ancha_hip_separate_workspace(const ancha_hip_roformer* m, size_t samples)
 
 namespace {
 
-// The first check flag in the order the reference runtime meets them, as its message.
+// The first check flag in the order the reference runtime meets them within one chunk, as its
+// message: Stft::forward's input check, the model output check of runtime.rs:172-176, then
+// Stft::inverse's coverage and output checks (dsp.rs:126-133; they fire before
+// Accumulator::add's "non-finite chunk output", which can then never be reached), and
+// Accumulator::finish. The flags are ORed over the whole clip, so when two chunks fail in
+// different ways the message is that of the earlier kind here, not of the earlier chunk.
 const char* flag_message(unsigned flags) {
   if (flags & ancha::kFlagInput) return "non-finite STFT input";
   if (flags & ancha::kFlagMasks) return "non-finite model output";
   if (flags & ancha::kFlagIstftUncovered) return "iSTFT has an uncovered sample";
-  if (flags & ancha::kFlagChunk) return "non-finite chunk output";
+  if (flags & ancha::kFlagChunk) return "non-finite iSTFT output";
   return "uncovered overlap-add sample";
 }
 

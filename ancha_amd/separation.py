@@ -192,6 +192,16 @@ class Roformer:
             pass
 
 
+def chunk_plan(chunk_samples: int, overlap: int, samples: int) -> tuple[int, int]:
+    """(chunks, border) of the separation of a `samples`-sample clip: ChunkPlan::new / starts
+    (crates/ancha-audio/src/chunk.rs:9-24) with the border rule of src/runtime.rs:103-111.
+    Raises ValueError for an invalid chunk or overlap divisor."""
+    chunks, border = ctypes.c_size_t(0), ctypes.c_size_t(0)
+    _native.check(_native.lib().ancha_hip_chunk_plan(chunk_samples, overlap, samples,
+                                                     ctypes.byref(chunks), ctypes.byref(border)))
+    return chunks.value, border.value
+
+
 def stft(signal: torch.Tensor, hop: int) -> torch.Tensor:
     """Stft::forward of both channels of signal [2, samples] -> [frames, 1025, 2, 2]
     (frame, bin, channel, re/im)."""

@@ -214,6 +214,17 @@ int ancha_hip_roformer_forward(ancha_hip_roformer *model, const float *spectrum,
                                void *workspace, size_t workspace_bytes, float *masks,
                                const volatile int *cancelled, hipStream_t stream);
 
+/* The chunk plan ancha_hip_separate runs for a clip of `samples` samples per channel: chunks
+ * of `chunk_samples` start every chunk_samples / overlap samples across the clip plus a
+ * reflected border of chunk_samples - step samples on each side (0 when the clip is not longer
+ * than two borders). Writes the chunk count (the reference's `report.chunks`, 0 for an empty
+ * clip) and the border to the non-NULL pointers. Host only. ANCHA_HIP_INVALID for a zero chunk,
+ * a zero overlap or overlap > chunk_samples ("invalid chunk or overlap divisor").
+ * Replaces `ChunkPlan::new` / `ChunkPlan::starts` (crates/ancha-audio/src/chunk.rs:9-24) and the
+ * border rule of src/runtime.rs:103-111. */
+int ancha_hip_chunk_plan(size_t chunk_samples, size_t overlap, size_t samples, size_t *chunks,
+                         size_t *border);
+
 /* Device bytes of the workspace ancha_hip_separate needs for a clip of `samples` samples. */
 size_t ancha_hip_separate_workspace(const ancha_hip_roformer *model, size_t samples);
 

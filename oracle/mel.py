@@ -192,6 +192,18 @@ def chunk_weight(samples: int, i: np.ndarray, first: bool, last: bool) -> np.nda
     return w
 
 
+def chunk_starts(chunk_samples, overlap, n):
+    """(starts, border) of the chunk loop for an n-sample clip: ChunkPlan::new and ::starts
+    (crates/ancha-audio/src/chunk.rs:9-24) over the clip plus the reflected border of
+    src/runtime.rs:103-111 (no border when n <= 2 * border)."""
+    if not (chunk_samples > 0 and overlap > 0 and overlap <= chunk_samples):
+        raise ValueError("invalid chunk or overlap divisor")
+    step = chunk_samples // overlap
+    border = chunk_samples - step
+    border = border if n > 2 * border else 0
+    return list(range(0, n + 2 * border, step)), border
+
+
 def separate(audio, config, weights, threads=1, chunks=None):
     """The chunked separation loop of src/runtime.rs:103-238 on stereo audio [2, n]:
     reflect-bordered chunks of chunk_samples every chunk_samples/overlap samples, STFT per
@@ -200,11 +212,8 @@ def separate(audio, config, weights, threads=1, chunks=None):
     audio = np.asarray(audio, np.float32)
     n = audio.shape[1]
     cs, n_fft, hop = config["chunk_samples"], config["n_fft"], config["hop"]
-    step = cs // config["overlap"]
-    border = cs - step
-    border = border if n > 2 * border else 0
+    starts, border = chunk_starts(cs, config["overlap"], n)
     length = n + 2 * border
-    starts = list(range(0, length, step))
     if chunks is not None:
         starts = starts[:chunks]
     stems = len(weights["masks"])

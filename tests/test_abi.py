@@ -20,7 +20,13 @@ def declared(path):
 
 @pytest.fixture(scope="module")
 def lib():
-    return _native.lib()
+    l = _native.lib()
+    # These checks hand host buffers to entry points whose argument checks must refuse them
+    # before any launch; where a gfx950 device is visible a broken check would launch a kernel
+    # on host memory, so they run only where none is.
+    if l.ancha_hip_available():
+        pytest.skip("host-buffer argument checks run only where no gfx950 device is visible")
+    return l
 
 
 def test_library_exports_every_declared_symbol(lib):

@@ -268,6 +268,30 @@ def test_block_ragged_sequence_lengths(gpu, tokens):
     assert err < 2e-3
 
 
+@pytest.mark.parametrize("dim,hidden,tokens,normalized", [
+    (256, 1024, 1301, True),     # the reference's deux model (configs/deux.json): time pass
+    (256, 1024, 60, False),      # its band pass (60 bands), no output norm
+    (128, 512, 801, False),      # dim 128 with 8 heads (inner 512 > dim)
+    (128, 512, 61, True),
+])
+def test_block_eight_heads_small_dims(gpu, dim, hidden, tokens, normalized):
+    """The fused QKV projection and block tail at dim 256 and dim 128 with 8 heads of 64 (the
+    qkv_kernel<16> / <8> and block_tail_kernel<2, 512> / <1, 512> instantiations), against the
+    oracle's kernel-path block (roformer.rs:464-520)."""
+    heads, groups = 8, 2
+    w = _block_weights(dim, heads, hidden, normalized=normalized)
+    x = W.normal((groups, tokens, dim), 80 + dim + tokens, 1.0)
+    block = roformer.Transformer(w, gpu)
+    xd = dev(x, gpu)
+    table = roformer.axis_rope(w["freqs"], tokens, gpu)
+    got = block(xd, table).cpu().numpy()
+    want = O.transformer_forward(w, x, kernels=True, threads=8)
+    err = float(np.abs(got - want).max())
+    print(f"block dim {dim} x 8 heads, T={tokens}: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
+    assert torch.equal(block(xd, table), block(xd, table))
+
+
 def test_block_wide_rows(gpu):
     """dim 640 (> 512): the fp16 operand kernel's multi-pass row path."""
     dim, heads, hidden, groups, tokens = 640, 4, 1280, 2, 70
