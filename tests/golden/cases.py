@@ -165,5 +165,56 @@ def production_case(name, device=None):
     return config, tensors, spectrum
 
 
+# Separations at production depth through the whole runtime (chunking, STFT, forward, masked
+# iSTFT, overlap-add), stems kept on a sample lattice plus whole-output moments:
+#   mel_karaoke_d6_sep: Mel-Karaoke, depth 6, a clip of exactly one 801-frame chunk's step
+#                       (88 200 samples: no border, one chunk start);
+#   bs_large_d2_sep:    BS-RoFormer-large, depth 2, a clip of one chunk length (485 100 samples:
+#                       no border, two chunk starts, batched through one forward).
+# name -> (bundled config, depth, weight seed, audio seed, clip samples)
+SEPARATIONS = {
+    "mel_karaoke_d6_sep": ("mel_karaoke", 6, 81, 82, 88_200),
+    "bs_large_d2_sep": ("bs_roformer_large", 2, 83, 84, 485_100),
+}
+SEPARATION_SAMPLE_STEP = 29
+
+
+def separation_case(name, device=None):
+    """(config, checkpoint tensors, audio [2, samples]); with a torch `device` the weight
+    stream is generated there (same values)."""
+    from ancha_amd import separation as S
+    bundled, depth, seed, audio_seed, samples = SEPARATIONS[name]
+    config = dict(S.load_config(bundled), depth=depth)
+    tensors = W.roformer_tensors(config, seed=seed, device=device)
+    return config, tensors, W.audio(samples, seed=audio_seed)
+
+
+def separation_index(samples):
+    return np.arange(0, samples, SEPARATION_SAMPLE_STEP)
+
+
+# The reference's bundled deux model (configs/deux.json: Mel-RoFormer with the Mel-Karaoke
+# band table, dim 256, 8 heads, 2 stems, 573 300-sample chunks = 1301 frames) at depth 1.
+DEUX = {"deux_d1": (1, 87, 88)}
+
+
+def deux_config(depth):
+    from ancha_amd import separation as S
+    return dict(S.load_config("mel_karaoke"), dim=256, depth=depth, chunk_samples=573_300,
+                overlap=2, stems=["vocals", "instrumental"])
+
+
+def deux_case(name, device=None):
+    """(config, checkpoint tensors, packed spectrum [1301, 4100])."""
+    import oracle.mel as M
+    depth, seed, audio_seed = DEUX[name]
+    config = deux_config(depth)
+    tensors = W.roformer_tensors(config, seed=seed, device=device)
+    chunk = W.audio(config["chunk_samples"], seed=audio_seed)
+    spectrum = M.pack_spectra([M.stft(chunk[c], config["n_fft"], config["hop"])
+                               for c in range(2)])
+    return config, tensors, spectrum
+
+
 def production_index(frames):
     return np.arange(0, 2050, PRODUCTION_ROW_STEP), np.arange(0, frames, PRODUCTION_FRAME_STEP)

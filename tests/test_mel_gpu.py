@@ -230,6 +230,53 @@ def test_forward_production_shapes_match_oracle(gpu, name):
     model.close()
 
 
+@pytest.mark.parametrize("name", sorted(C.SEPARATIONS))
+def test_production_separation_matches_oracle(gpu, name):
+    """The separated stems at production depth against the oracle's separation loop
+    (runtime.rs:103-238 restated in oracle.mel.separate, tests/golden/production_separations.npz):
+    Mel-Karaoke at depth 6 on a one-chunk clip, BS-RoFormer-large at depth 2 on a two-chunk clip
+    batched through one forward. The end-to-end gate is 50 dB (scripts/verify_parity.py:93 of the
+    reference), measured on a sample lattice plus the whole output's sum of squares."""
+    config, tensors, audio = C.separation_case(name, device=gpu)
+    f = fixture("production_separations.npz")
+    np.testing.assert_allclose(C.checksum(audio, *(tensors[k] for k in sorted(tensors))),
+                               f[f"checksum_{name}"], rtol=1e-12)
+    model = S.Roformer(config, tensors, gpu)
+    stems, residual = model.separate(torch.from_numpy(audio).to(gpu))
+    got = stems.cpu().numpy()
+    db = snr_db(f[name], got[..., C.separation_index(audio.shape[1])])
+    report(f"{name} stems vs oracle SNR dB", db)
+    assert db > 50.0
+    m, want = C.moments(got), f[f"moments_{name}"]
+    report(f"{name} sum of squares rel. diff", abs(m[1] - want[1]) / want[1])
+    assert abs(m[1] - want[1]) < 1e-3 * want[1]
+    if residual is not None:
+        np.testing.assert_allclose(residual.cpu().numpy(), audio - got[0], atol=1e-6)
+    model.close()
+
+
+@pytest.mark.parametrize("name", sorted(C.DEUX))
+def test_forward_deux_shape_matches_oracle(gpu, name):
+    """The reference's deux model shape (dim 256, 8 heads, 2 stems, Mel-Karaoke bands, 1301
+    frames) at depth 1 against the oracle's masks (tests/golden/deux_network.npz): the dim-256
+    fused QKV and tail, the 1301-frame time pass (three query blocks per sequence), the
+    dim-256 band split and the x4 mask heads."""
+    config, tensors, spectrum = C.deux_case(name, device=gpu)
+    f = fixture("deux_network.npz")
+    np.testing.assert_allclose(C.checksum(spectrum, *(tensors[k] for k in sorted(tensors))),
+                               f[f"checksum_{name}"], rtol=1e-12)
+    model = S.Roformer(config, tensors, gpu)
+    got = model(torch.from_numpy(spectrum).to(gpu)).cpu().numpy()
+    assert got.shape == (2, 2050, 2, 1301)
+    rows, frames = C.production_index(spectrum.shape[0])
+    db = snr_db(f[name], got[:, rows][..., frames])
+    report(f"{name} forward vs oracle SNR dB", db)
+    assert db > 50.0
+    m, want = C.moments(got), f[f"moments_{name}"]
+    assert abs(m[1] - want[1]) < 1e-3 * want[1]
+    model.close()
+
+
 def composed_separation(model, audio, config):
     """The chunk loop of runtime.rs:103-238 written out on the host from the library's single
     pieces (GPU STFT, one-chunk forward, masked iSTFT) and the oracle's overlap-add: the
@@ -342,6 +389,55 @@ def test_separate_reports_non_finite_model_output(gpu):
     model = S.Roformer(config, tensors, gpu)
     with pytest.raises(ValueError, match="non-finite model output"):
         model.separate(torch.from_numpy(W.audio(60_000, seed=66)).to(gpu))
+
+
+def test_separate_reports_non_finite_istft_output(gpu):
+    """Finite masks that overflow the masked spectrum: Stft::inverse's "non-finite iSTFT output"
+    (dsp.rs:132-133), reported before the overlap-add (chunk.rs:57-60)."""
+    config = tiny_config(stems=("vocals",))
+    tensors = W.roformer_tensors(config, seed=65)
+    # A value column of band 1's GLU: masks of ~1e38 stay finite, mask * spectrum does not.
+    tensors["mask_estimators.0.to_freqs.1.0.4.bias"][7] = np.float32(3e38)
+    model = S.Roformer(config, tensors, gpu)
+    spec = torch.from_numpy(packed_spectrum(W.audio(44_100, seed=66), config["hop"])).to(gpu)
+    assert torch.isfinite(model(spec)).all()
+    with pytest.raises(ValueError, match="non-finite iSTFT output"):
+        model.separate(torch.from_numpy(W.audio(60_000, seed=66)).to(gpu))
+    assert _native.lib().ancha_hip_check() == 0
+
+
+def test_cancel_from_another_thread_during_separation(gpu):
+    """The CancelFlag set by another thread while ancha_hip_separate runs: the call returns
+    "task cancelled" at its next check (between chunk pairs, layer pairs and mask heads), after
+    the work it enqueued has finished; the model stays usable and an uncancelled run of the
+    same clip is unchanged."""
+    import threading
+
+    config = tiny_config(stems=("vocals",), depth=2)
+    model = S.Roformer(config, W.roformer_tensors(config, seed=71), gpu)
+    audio = torch.from_numpy(W.audio(40 * 44_100, seed=72)).to(gpu)
+    reference, _ = model.separate(audio)
+    torch.cuda.synchronize()
+    cancelled = 0
+    for delay in (0.0, 0.001, 0.004):
+        flag = S.CancelFlag()
+        timer = threading.Timer(delay, flag.set)
+        timer.start()
+        try:
+            stems, _ = model.separate(audio, cancelled=flag)
+            # The loop finished before it saw the flag: the result is the whole separation.
+            assert torch.equal(stems, reference)
+        except _native.Cancelled as e:
+            assert "task cancelled" in str(e)
+            cancelled += 1
+        timer.join()
+        torch.cuda.synchronize()
+    report("separations cancelled mid-run", cancelled)
+    assert cancelled >= 1
+    assert _native.lib().ancha_hip_check() == 0
+    stems, _ = model.separate(audio)
+    assert torch.equal(stems, reference)
+    model.close()
 
 
 def test_cancelled_separation_and_forward(gpu):
