@@ -48,8 +48,9 @@ __device__ __forceinline__ OutRows out_rows(const AttnParams& p, int g, int h) {
 }
 
 // Long sequences (T > 64) on v_mfma_f32_32x32x16_f16: 16 waves x 32 queries per workgroup.
-// Aligned calls with head_dim 64 only (every call the library makes): fp32 q / k / v, or the
-// block's fp16 projection (in_half).
-hipError_t launch_attention_long(const AttnParams& p, bool gated, bool rope, hipStream_t stream);
+// fp32 q / k / v (`aligned`: rows, table and output 16-byte aligned; otherwise 4-byte accesses),
+// or the block's fp16 projection (in_half, aligned only).
+hipError_t launch_attention_long(const AttnParams& p, bool gated, bool rope, bool aligned,
+                                 hipStream_t stream);
 
 }  // namespace ancha

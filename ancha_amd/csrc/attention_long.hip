@@ -134,7 +134,17 @@ __device__ __forceinline__ void load_lds16(rsrc_t r, unsigned char* dst, unsigne
                                            off, 0, 0, 0);
 }
 
-template <bool GATED, bool ROPE, bool XH>
+// The same with 4 bytes per lane: lane l's dword at `off` lands at dst + 4 * l.
+__device__ __forceinline__ void load_lds4(rsrc_t r, unsigned char* dst, unsigned off) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 4,
+                                           off, 0, 0, 0);
+}
+
+// ALIGNED: q / k / v rows and the output are 16-byte aligned (every call the library itself
+// makes); otherwise their accesses are 4-byte ones (rows of an odd column count, e.g. a packed
+// projection with 1549 columns), with the same tiles and walk. TALIGNED: the same for the
+// rotary table.
+template <bool GATED, bool ROPE, bool XH, bool ALIGNED, bool TALIGNED = ALIGNED>
 __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnParams p, int qblocks,
                                                                         int passes) {
   // K tile: row = key (128 bytes of fp16 channels); V^T tile: row = channel (64 keys in
@@ -211,8 +221,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
         kh = __builtin_amdgcn_raw_buffer_load_b64(kr, (unsigned)skey * ldk4 + sc * 8, 0, 0);
         vh = __builtin_amdgcn_raw_buffer_load_b64(vr, (unsigned)skey * ldv4 + sc * 8, 0, 0);
       } else {
-        kx = bload4<true>(kr, (unsigned)skey * ldk4 + sc * 16);
-        vx = bload4<true>(vr, (unsigned)skey * ldv4 + sc * 16);
+        kx = bload4<ALIGNED>(kr, (unsigned)skey * ldk4 + sc * 16);
+        vx = bload4<ALIGNED>(vr, (unsigned)skey * ldv4 + sc * 16);
       }
     }
     if constexpr (ROPE && !XH) {
@@ -220,8 +230,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
         // Key cos rows (table 2) and sign-folded sin rows (table 3) of this tile.
         const rsrc_t cr = make_rsrc(p.rope + (long)(2 * T + key0) * 64, rows * 256);
         const rsrc_t sr = make_rsrc(p.rope + (long)(3 * T + key0) * 64, rows * 256);
-        kc = bload4<true>(cr, (unsigned)skey * 256 + sc * 16);
-        ks = bload4<true>(sr, (unsigned)skey * 256 + sc * 16);
+        kc = bload4<TALIGNED>(cr, (unsigned)skey * 256 + sc * 16);
+        ks = bload4<TALIGNED>(sr, (unsigned)skey * 256 + sc * 16);
       }
     }
   };
@@ -276,10 +286,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
 #pragma unroll
       for (int it = 0; it < 8; it++) {
         const int r = (lane >> 4) + 4 * it, c = lane & 15;
-        float4 x = bload4<true>(qr, (unsigned)r * ldq4 + c * 16);
+        float4 x = bload4<ALIGNED>(qr, (unsigned)r * ldq4 + c * 16);
         if constexpr (ROPE)
-          x = rotate4(x, bload4<true>(cr, (unsigned)r * 256 + c * 16),
-                      bload4<true>(sr, (unsigned)r * 256 + c * 16));
+          x = rotate4(x, bload4<TALIGNED>(cr, (unsigned)r * 256 + c * 16),
+                      bload4<TALIGNED>(sr, (unsigned)r * 256 + c * 16));
         x = scale4(x, kLog2e);
         *reinterpret_cast<u32x2*>(Q + row_offset(r, c >> 1) + ((c & 1) << 3)) =
             u32x2{pack_h2(x.x, x.y), pack_h2(x.z, x.w)};
@@ -297,7 +307,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
       const int r = 8 * c + (lane >> 3);
       const int cc = (lane & 7) ^ ((r >> 1) & 7);
       load_lds16(qr, lds_q[wave] + 1024 * c, (unsigned)r * ldq4 + cc * 16);
-    } else {
+    } else if constexpr (ALIGNED) {
       // Rows 4 c + l / 16, 16-byte piece l % 16: query row, then cos and sin table rows.
       const int r = 4 * c + (lane >> 4), cc = lane & 15;
       unsigned char* R = lds_raw[wave];
@@ -306,6 +316,27 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
         const unsigned rows = (unsigned)(T - q0);
         const rsrc_t cr = make_rsrc(p.rope + (long)q0 * 64, rows * 256);
         const rsrc_t sr = make_rsrc(p.rope + (long)(T + q0) * 64, rows * 256);
+        load_lds16(cr, R + 1024, (unsigned)r * 256 + cc * 16);
+        load_lds16(sr, R + 2048, (unsigned)r * 256 + cc * 16);
+      }
+    } else {
+      // Query rows as four dword loads, row 4 c + i each (lane l: float l): the same LDS layout;
+      // the table rows as above when the table is aligned.
+      unsigned char* R = lds_raw[wave];
+      const unsigned rows = (unsigned)(T - q0);
+      const rsrc_t cr = make_rsrc(ROPE ? p.rope + (long)q0 * 64 : p.q, ROPE ? rows * 256 : 0);
+      const rsrc_t sr = make_rsrc(ROPE ? p.rope + (long)(T + q0) * 64 : p.q, ROPE ? rows * 256 : 0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const unsigned r = (unsigned)(4 * c + i);
+        load_lds4(qr, R + 256 * i, r * ldq4 + lane * 4);
+        if constexpr (ROPE && !TALIGNED) {
+          load_lds4(cr, R + 1024 + 256 * i, r * 256 + lane * 4);
+          load_lds4(sr, R + 2048 + 256 * i, r * 256 + lane * 4);
+        }
+      }
+      if constexpr (ROPE && TALIGNED) {
+        const int r = 4 * c + (lane >> 4), cc = lane & 15;
         load_lds16(cr, R + 1024, (unsigned)r * 256 + cc * 16);
         load_lds16(sr, R + 2048, (unsigned)r * 256 + cc * 16);
       }
@@ -525,7 +556,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
             __builtin_amdgcn_raw_buffer_store_b64(u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)},
                                                   out.out, (unsigned)t * out.ld4 + c * 2, 0, 0);
           else
-            bstore4<true>(out.out, (unsigned)t * out.ld4 + c * 4, v);
+            bstore4<ALIGNED>(out.out, (unsigned)t * out.ld4 + c * 4, v);
         }
     }
     // The next pass's first tile and query rows are in place; this pass's tiles are free.
@@ -534,7 +565,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
   }
 }
 
-template <bool GATED, bool ROPE, bool XH>
+template <bool GATED, bool ROPE, bool XH, bool ALIGNED = true, bool TALIGNED = ALIGNED>
 hipError_t launch_t(const AttnParams& p, hipStream_t stream) {
   const int qblocks = (p.tokens + kQueries - 1) / kQueries;
   const int passes = p.groups * p.heads * qblocks;
@@ -542,18 +573,30 @@ hipError_t launch_t(const AttnParams& p, hipStream_t stream) {
   // passes run one per workgroup (the walk would only lengthen the critical path).
   const int cus = device_cus();
   const int grid = passes <= 2 * cus ? passes : cus;
-  hipLaunchKernelGGL((attention_long_kernel<GATED, ROPE, XH>), dim3(grid), dim3(kWaves * 64), 0,
-                     stream, p, qblocks, passes);
+  hipLaunchKernelGGL((attention_long_kernel<GATED, ROPE, XH, ALIGNED, TALIGNED>), dim3(grid),
+                     dim3(kWaves * 64), 0, stream, p, qblocks, passes);
   return hipGetLastError();
 }
 
 }  // namespace
 
-hipError_t launch_attention_long(const AttnParams& p, bool gated, bool rope, hipStream_t stream) {
+hipError_t launch_attention_long(const AttnParams& p, bool gated, bool rope, bool aligned,
+                                 hipStream_t stream) {
   if (p.tokens <= 64) return hipErrorInvalidValue;
   if (p.in_half) {
-    if (!gated || rope) return hipErrorInvalidValue;
+    if (!gated || rope || !aligned) return hipErrorInvalidValue;
     return launch_t<true, false, true>(p, stream);
+  }
+  if (!aligned) {
+    // Rows not 16-byte aligned; the table (256-byte rows) is aligned when its base is.
+    const bool table_aligned = (reinterpret_cast<uintptr_t>(p.rope) & 15) == 0;
+    if (rope)
+      return gated ? (table_aligned ? launch_t<true, true, false, false, true>(p, stream)
+                                    : launch_t<true, true, false, false, false>(p, stream))
+                   : (table_aligned ? launch_t<false, true, false, false, true>(p, stream)
+                                    : launch_t<false, true, false, false, false>(p, stream));
+    return gated ? launch_t<true, false, false, false>(p, stream)
+                 : launch_t<false, false, false, false>(p, stream);
   }
   if (gated) return rope ? launch_t<true, true, false>(p, stream) : launch_t<true, false, false>(p, stream);
   return rope ? launch_t<false, true, false>(p, stream) : launch_t<false, false, false>(p, stream);

@@ -90,11 +90,12 @@ def test_model_and_dsp_entry_points_check_arguments(lib):
 
 
 def test_attention_grid_guard(lib):
-    """A problem count whose launch would exceed HIP's 2^32-thread grid is UNSUPPORTED (the
-    caller falls back) instead of a launch failure that would poison the sticky state."""
+    """A problem count the launch cannot index (a short-sequence grid past HIP's 2^32 threads, or
+    more than 2^31 long-sequence passes of 512 queries) is UNSUPPORTED (the caller falls back)
+    instead of a launch failure that would poison the sticky state."""
     buf = ctypes.create_string_buffer(1 << 12)
     p = ctypes.addressof(buf)
-    for groups, tokens in ((1 << 22, 801), (1 << 25, 60)):
+    for groups, tokens in ((1 << 27, 801), (1 << 25, 60)):
         rc = lib.ancha_hip_attention(p, p, p, groups, tokens, 8, 512, 512, 512, None, p, None)
         assert rc == _native.UNSUPPORTED and "exceeds the grid" in _native.last_error()
     assert lib.ancha_hip_check() == 0

@@ -111,10 +111,12 @@ def test_rope_on_load_matches_oracle(gpu, tokens):
     check(f"rope T={tokens}", got, expected)
 
 
-@pytest.mark.parametrize("tokens", [60, 130, 801])
-def test_gated_rope_on_unaligned_packed_rows(gpu, tokens):
+@pytest.mark.parametrize("tokens,table_offset", [(60, 0), (130, 0), (801, 0), (130, 1), (801, 1)])
+def test_gated_rope_on_unaligned_packed_rows(gpu, tokens, table_offset):
     # RoPE on load with rows whose stride is not a multiple of 4 floats (q | k | v | gates |
-    # 6 zero columns: 585 per row): the element-wise load path of both attention kernels.
+    # 6 zero columns: 585 per row): the element-wise load path of both attention kernels; with
+    # table_offset 1 the rotary table also starts 4 bytes past a 16-byte boundary (its rows are
+    # then read element-wise too).
     groups, heads = 2, 3
     q, k, v = (W.normal_torch((groups, tokens, heads, 64), s, 1.0, device=gpu) for s in (5, 6, 7))
     gates = W.normal_torch((groups, tokens, heads), 8, 2.0, device=gpu)
@@ -123,11 +125,16 @@ def test_gated_rope_on_unaligned_packed_rows(gpu, tokens):
                         torch.zeros((groups, tokens, 6), device=gpu)], dim=2)
     assert packed.shape[2] % 4 != 0
     table = W.axis_rope_packed(W.rope_freqs(), tokens)
-    got = fused.gated_attention(packed, heads, rope=dev(table, gpu))
+    store = torch.zeros(table.size + table_offset, device=gpu)
+    store[table_offset:] = dev(table.ravel(), gpu)
+    table_dev = store[table_offset:].view(table.shape)
+    assert (table_dev.data_ptr() % 16 == 0) == (table_offset == 0)
+    got = fused.gated_attention(packed, heads, rope=table_dev)
     assert got is not None
     expected = O.attention_op(q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy(), rope=table)
     expected = expected / (1.0 + np.exp(-gates.cpu().numpy().astype(np.float64)))[..., None]
-    check(f"gated rope unaligned T={tokens}", got.cpu().numpy(), expected)
+    check(f"gated rope unaligned T={tokens} table offset {table_offset}", got.cpu().numpy(),
+          expected)
 
 
 def test_rope_on_load_equals_prerotated_inputs(gpu):
