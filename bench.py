@@ -44,13 +44,13 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def profiled_traffic(workload: str):
-    """HBM bytes per launch of the attention kernel from the committed counter summary
-    (profiles/attention_<workload>_*.md: FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
+def profiled_traffic(pattern: str, key: str = "traffic_bytes_per_launch"):
+    """HBM bytes per launch (attention ops) or per step (layer pair, separations) from the
+    committed counter summary profiles/<pattern> (FETCH_SIZE + WRITE_SIZE, copy-calibrated)."""
     import glob
-    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"attention_{workload}_*.md"))):
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", pattern))):
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
+            if line.startswith(key + ":"):
                 return int(line.split(":")[1])
     return None
 
@@ -211,7 +211,8 @@ def layer_result(steps, warmup, no_cpu_baseline, torch, dev) -> dict:
                    "gflop_per_step": round(flops / 1e9, 2), "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
-                     "traffic": None, "scope": "whole layer pair (all kernels)"},
+                     "traffic": profiled_traffic("layer_pair_*.md", "traffic_bytes_per_step"),
+                     "scope": "whole layer pair (all kernels); traffic = HBM bytes per step"},
     }
     if not no_cpu_baseline:
         log("timing the restated reference CPU path (Burn-path block) on sampled groups")
@@ -271,11 +272,12 @@ SEPARATIONS = {
     # workload: (bundled config, clip seconds, metric, config description)
     "mel": ("mel_karaoke", 30, "audio-seconds/sec for Mel-RoFormer fwd",
             "Mel-RoFormer separation (Mel-Karaoke: 60 bands, dim 384, depth 6, 8x64 heads, "
-            "chunk 352800 / overlap 4) of a 30 s clip"),
+            "chunk 352800 / overlap 4, two chunks per forward) of a 30 s clip"),
     "bs": ("bs_roformer_large", 300, "audio-seconds/sec for BS-RoFormer-large fwd",
            "BS-RoFormer-large separation (62 bands, dim 512, depth 12, 8x64 heads, chunk 485100 "
-           "/ overlap 2, chunks one after another) of a 5 min clip"),
+           "/ overlap 2, two chunks per forward) of a 5 min clip"),
 }
+SEPARATION_PROFILES = {"mel": "mel_separation_*.md", "bs": "bs_roformer_large_*.md"}
 
 
 # The reference's own published CPU speed on this model (Flex backend, batched), for context
@@ -345,7 +347,9 @@ def separation_result(workload, steps, warmup, no_cpu_baseline, torch, dev) -> d
                    "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
-                     "traffic": None, "scope": "whole separation (all kernels)"},
+                     "traffic": profiled_traffic(SEPARATION_PROFILES[workload],
+                                                 "traffic_bytes_per_step"),
+                     "scope": "whole separation (all kernels); traffic = HBM bytes per clip"},
     }
     if not no_cpu_baseline:
         import oracle.mel as OM
@@ -511,12 +515,12 @@ def attention_result(workload, steps, warmup, no_cpu_baseline, tokens, copy_cal,
         achieved = flops / (kernel_ms * 1e-3) / 1e12
         roofline = {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_MFMA_TFLOPS,
                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_MFMA_TFLOPS, 4),
-                    "traffic": profiled_traffic("time") if default_shape else None}
+                    "traffic": profiled_traffic("attention_time_*.md") if default_shape else None}
     else:
         achieved = io_bytes / (kernel_ms * 1e-3) / 1e9
         roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": profiled_traffic("band") if default_shape else None}
+                    "traffic": profiled_traffic("attention_band_*.md") if default_shape else None}
     result = {
         "metric": "fused attn TFLOP/s (% MFMA peak)",
         "value": round(value, 3),
