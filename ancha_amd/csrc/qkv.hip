@@ -3,16 +3,27 @@
 //   out[r][c] = epilogue(sum_k xh[r][k] W^T[c][k] + bias[c]), fp16,
 // with the interleaved rotary embedding on columns [0, 2 width) (queries, then keys, of token
 // (r / token_div) % tokens) and the queries also times q_scale (log2 e for the exp2 softmax).
+// Only the columns that hold values are computed and written: q, k, v and the heads' gate
+// logits, 3 width + width / 64 of them, rounded up to a 32-column block; the packed layout's
+// zero padding after them is never read by the attention kernels and is left as it is.
 //
 // 128 rows per workgroup: their fp16 operand rows sit in LDS for the whole block as B
 // fragments of v_mfma_f32_32x32x16_f16 (straight from HBM with direct-to-LDS loads), with the
-// rows' rotary cos / sin (32 + 32 per row) next to them. The 8 waves walk the output in 32-column
-// blocks (wave w takes blocks w, w + 8, ..., so each SIMD gets the same count); per block a wave
-// accumulates all 128 rows (4 x 32-row MFMA tiles) over K, reading each weight A fragment once
-// (a contiguous kilobyte of the fragment-major W^T) for four MFMAs, then rotates and stores its
-// 32 x 128 tile straight from the accumulators (lane l owns row l % 32, columns 8q + 4(l/32) ..
-// +3: both members of every rotary pair). No barriers inside the column walk, so the two waves
-// of a SIMD drift apart and one's epilogue runs beside the other's MFMAs.
+// rows' rotary cos / sin (32 + 32 per row) next to them. The 8 waves walk the output in pairs of
+// 32-column blocks (pair p on SIMD p % 4, so the SIMDs get the same count); per pair a wave
+// accumulates all 128 rows (4 x 32-row MFMA tiles per block) over K, so each operand B fragment
+// read from LDS feeds two MFMAs and each weight A fragment (a contiguous kilobyte of the
+// fragment-major W^T) four. The epilogue takes one 32-row tile of the pair at a time: bias,
+// rotary and query scale on the accumulators (lane l owns row l % 32, columns 8q + 4(l/32) .. +3
+// of each block: both members of every rotary pair), fp16 into a 4 KB staging area of the wave,
+// read back so that each store covers 8 whole rows of the pair, i.e. whole 128-byte lines,
+// written non-temporally (the projection is read once, by the next kernel). Measured against
+// stores of 32-byte row pieces from the accumulators: the 320 MB output costs ~26 % of the
+// kernel that way, whole lines through the caches save 10 % of it, non-temporal whole lines 17 %.
+// An odd last block is split by row tile over the four waves of the first SIMD slots. No
+// barriers inside the column walk, so the two waves of a SIMD drift apart and one's epilogue
+// runs beside the other's MFMAs. At dim 512 the operand rows and tables of 128 rows fill the
+// LDS, and qkv_direct_kernel (below) stores from the accumulators instead.
 #include "buffer.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -20,13 +31,230 @@
 namespace ancha {
 namespace {
 
-constexpr int kRows = 128;
 constexpr int kWaves = 8;
 constexpr int kFrag = 1024;
 
-// SD = dim / 16 k steps.
-template <int SD>
+// SD = dim / 16 k steps (dims 128, 256, 384); NR = 4 32-row tiles per row block.
+template <int SD, int NR>
 __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
+  constexpr int kRows = 32 * NR;
+  constexpr int kX = kRows * SD * 16 * 2;      // operand fragments
+  // Per row: 16 chunks of (cos, sin) for two rotary pairs, chunk c at position c ^ (row & 15)
+  // (rows 256 bytes apart would otherwise put one column's reads of 32 rows in one bank).
+  constexpr int kT = kRows * 64 * 4;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kX + kT];
+  float* const cs = reinterpret_cast<float*>(lds + kX);
+  // Per wave: one row tile of a pair's output, 32 rows x 128 bytes, 16-byte chunk c of row r at
+  // position c ^ (r & 7), so a wave's stores leave as whole 128-byte lines (8 rows per store).
+  __shared__ __attribute__((aligned(16))) unsigned char stage[kWaves][32 * 128];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5, col = lane & 31;
+  const unsigned lane16 = (unsigned)lane * 16;
+  const int dim = SD * 16;
+  const int used = 3 * p.width + p.width / 64;   // q, k, v and one gate column per head
+  const int blocks = (used + 31) / 32;
+  const int pairs = blocks / 2;
+  const bool odd = (blocks & 1) != 0;
+  const rsrc_t wr = make_rsrc(p.w, (unsigned)(p.cols * dim * 2));
+  const rsrc_t br = make_rsrc(p.bias, (unsigned)(p.cols * 4));
+  const rsrc_t tr = make_rsrc(p.rope, (unsigned)(4 * p.tokens * 256));
+
+  auto load_bias = [&](int b, float4 (&bias)[4]) {
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+      bias[q] = __builtin_bit_cast(
+          float4, __builtin_amdgcn_raw_buffer_load_b128(br, 16 * half,
+                                                        (unsigned)(32 * b + 8 * q) * 4, 0));
+  };
+  // Bias -> rotary -> query scale (fused/gemm.rs:46-82 order) of row tile j of output block b,
+  // as fp16: packed[q] holds this lane's row 32 j + l % 32, columns 8 q + 4 (l / 32) .. + 3.
+  auto tile_values = [&](const f32x16& acc, int b, int j, const float4 (&bias)[4],
+                         u32x2 (&packed)[4]) {
+    const bool rq = 32 * b < p.width, rk = !rq && 32 * b < 2 * p.width;
+    const int r = 32 * j + col;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int pair = ((32 * b + 8 * q + 4 * half) & 63) >> 1;
+      float4 v = make_float4(acc[4 * q] + bias[q].x, acc[4 * q + 1] + bias[q].y,
+                             acc[4 * q + 2] + bias[q].z, acc[4 * q + 3] + bias[q].w);
+      if (rq || rk) {
+        // (cos, sin) of pairs `pair` and `pair` + 1 (one 16-byte chunk).
+        const float4 t = *reinterpret_cast<const float4*>(
+            cs + r * 64 + (((pair >> 1) ^ (r & 15)) << 2));
+        // Pair (c, c+1): y_c = x_c cos - x_{c+1} sin, y_{c+1} = x_{c+1} cos + x_c sin.
+        float4 y = make_float4(v.x * t.x - v.y * t.y, v.y * t.x + v.x * t.y,
+                               v.z * t.z - v.w * t.w, v.w * t.z + v.z * t.w);
+        if (rq) {
+          const float s = 0.125f * p.q_scale;
+          y = make_float4(y.x * s, y.y * s, y.z * s, y.w * s);
+        }
+        v = y;
+      }
+      packed[q] = u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
+    }
+  };
+
+  // Pairs of this wave: wave + 8 n (n < mine); pair index % 4 = wave % 4 = its SIMD.
+  const int mine = pairs > wave ? (pairs - wave + kWaves - 1) / kWaves : 0;
+  // k steps of weight fragments in flight (two fragments each); with four row tiles, four steps
+  // and the staging epilogue no longer fit the 256 registers of two waves per SIMD
+  constexpr int PD = 2;
+  static_assert(SD % PD == 0 && SD >= PD, "K steps come in groups of PD");
+
+  for (int blk = blockIdx.x; blk * kRows < p.rows; blk += gridDim.x) {
+    const int row0 = blk * kRows;
+    const int nrows = min(kRows, p.rows - row0);
+    const rsrc_t xr = make_rsrc(p.xh + (long)row0 * dim, (unsigned)(nrows * dim * 2));
+    const rsrc_t outr = make_rsrc(p.out + (long)row0 * p.cols, (unsigned)(nrows * p.cols * 2));
+    // Operand rows as B fragments: fragment (jb, s) = rows 32 jb + (l % 32), k 16 s + 8 (l / 32).
+    for (int f = wave; f < NR * SD; f += kWaves) {
+      const int jb = f / SD, s = f % SD;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          xr, (__attribute__((address_space(3))) void*)(lds + f * kFrag), 16,
+          ((unsigned)(32 * jb + col) * dim + 16 * s + 8 * half) * 2, 0, 0, 0);
+    }
+    // Key-table cos / sin of each row's token (the query tables are these times 1/8).
+    for (int e = tid; e < kRows * 32; e += kWaves * 64) {
+      const int r = e >> 5, i = e & 31;
+      const int tok = ((row0 + r) / p.token_div) % p.tokens;
+      float* slot = cs + r * 64 + (((i >> 1) ^ (r & 15)) << 2) + 2 * (i & 1);
+      slot[0] = bload1(tr, (unsigned)((2 * p.tokens + tok) * 64 + 2 * i) * 4);
+      slot[1] = bload1(tr, (unsigned)((3 * p.tokens + tok) * 64 + 2 * i + 1) * 4);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+
+    if (mine > 0) {
+      // The A fragments of block 2 pr (x = 0) and 2 pr + 1 (x = 1) stream through the ring
+      // across the wave's pairs.
+      u32x4 a[PD][2];
+#pragma unroll
+      for (int i = 0; i < PD; i++)
+#pragma unroll
+        for (int x = 0; x < 2; x++)
+          a[i][x] = __builtin_amdgcn_raw_buffer_load_b128(
+              wr, lane16, (unsigned)(((2 * wave + x) * SD + i) * kFrag), 0);
+      for (int n = 0; n < mine; n++) {
+        const int pr = wave + kWaves * n;
+        // The operand fragments are the same for every pair; an opaque per-pair offset keeps
+        // the compiler from hoisting all their LDS reads (NR * SD fragments) out of the loop.
+        int opaque = 0;
+        asm volatile("" : "+s"(opaque));
+        const unsigned char* X = lds + opaque;
+        f32x16 acc[2][NR];
+#pragma unroll
+        for (int x = 0; x < 2; x++)
+#pragma unroll
+          for (int j = 0; j < NR; j++) acc[x][j] = mfma32_zero();
+        // Fragment offsets of this pair's first block and of the next pair's (the last pair
+        // reloads itself: unconditional loads keep the ring in fixed registers).
+        const unsigned here = (unsigned)(2 * pr * SD * kFrag);
+        const unsigned next =
+            (unsigned)(2 * min(pr + kWaves, wave + kWaves * (mine - 1)) * SD * kFrag);
+#pragma unroll
+        for (int s = 0; s < SD; s++) {
+          u32x4 cur[2];
+#pragma unroll
+          for (int x = 0; x < 2; x++) {
+            cur[x] = a[s % PD][x];
+            const unsigned off = s + PD < SD ? here + (x * SD + s + PD) * kFrag
+                                             : next + (x * SD + s + PD - SD) * kFrag;
+            a[s % PD][x] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane16, off, 0);
+          }
+          // Operand reads and MFMAs of one step; the scheduling barrier keeps the compiler from
+          // pulling later steps' LDS reads forward.
+#pragma unroll
+          for (int j = 0; j < NR; j++) {
+            const u32x4 bf = *reinterpret_cast<const u32x4*>(X + (j * SD + s) * kFrag + lane16);
+#pragma unroll
+            for (int x = 0; x < 2; x++) acc[x][j] = mfma32(cur[x], bf, acc[x][j]);
+          }
+          if (s % 2 == 1) __builtin_amdgcn_sched_barrier(0);
+        }
+        float4 bias[2][4];
+#pragma unroll
+        for (int x = 0; x < 2; x++) load_bias(2 * pr + x, bias[x]);
+        unsigned char* const st = stage[wave];
+#pragma unroll
+        for (int j = 0; j < NR; j++) {
+#pragma unroll
+          for (int x = 0; x < 2; x++) {
+            u32x2 packed[4];
+            tile_values(acc[x][j], 2 * pr + x, j, bias[x], packed);
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+              *reinterpret_cast<u32x2*>(st + col * 128 + (((4 * x + q) ^ (col & 7)) << 4) +
+                                        8 * half) = packed[q];
+          }
+          // Rows 8 k + l / 8 of the tile, 16-byte chunk l % 8: whole 128-byte lines.
+#pragma unroll
+          for (int k = 0; k < 4; k++) {
+            const int rr = 8 * k + (lane >> 3);
+            const u32x4 w = *reinterpret_cast<const u32x4*>(
+                st + rr * 128 + (((lane & 7) ^ (rr & 7)) << 4));
+            __builtin_amdgcn_raw_buffer_store_b128(
+                w, outr, ((unsigned)(32 * j + rr) * p.cols + 8 * (lane & 7)) * 2,
+                (unsigned)(64 * pr) * 2, kStream);
+          }
+        }
+      }
+    }
+    if (odd && wave < NR) {
+      // The last block: row tile `wave` of it (one MFMA per k step).
+      const int b = blocks - 1, j = wave;
+      f32x16 acc = mfma32_zero();
+      u32x4 a[PD];
+#pragma unroll
+      for (int i = 0; i < PD; i++)
+        a[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane16, (unsigned)((b * SD + i) * kFrag),
+                                                     0);
+#pragma unroll
+      for (int s = 0; s < SD; s++) {
+        const u32x4 cur = a[s % PD];
+        if (s + PD < SD)
+          a[s % PD] = __builtin_amdgcn_raw_buffer_load_b128(
+              wr, lane16, (unsigned)((b * SD + s + PD) * kFrag), 0);
+        const u32x4 bf = *reinterpret_cast<const u32x4*>(lds + (j * SD + s) * kFrag + lane16);
+        acc = mfma32(cur, bf, acc);
+      }
+      float4 bias[4];
+      load_bias(b, bias);
+      u32x2 packed[4];
+      tile_values(acc, b, j, bias, packed);
+      // Lanes l and l + 32 trade halves (v_permlane32_swap) so each holds 8 consecutive columns
+      // of its row: one 16-byte store per lane covers 16 columns of 32 rows.
+      const int r = 32 * j + col;
+#pragma unroll
+      for (int qq = 0; qq < 4; qq += 2) {
+        // Low lanes: own columns 8(qq+1) .. +3 and the partner's 8(qq+1) + 4 .. +7; high lanes:
+        // the partner's 8 qq .. +3 and own 8 qq + 4 .. +7.
+        u32x4 w;
+#pragma unroll
+        for (int d = 0; d < 2; d++) {
+          const auto sw = __builtin_amdgcn_permlane32_swap(packed[qq + 1][d], packed[qq][d],
+                                                           false, false);
+          const unsigned lo = sw[0], hi = sw[1];
+          w[d] = lo;
+          w[2 + d] = hi;
+        }
+        __builtin_amdgcn_raw_buffer_store_b128(
+            w, outr, ((unsigned)r * p.cols + 8 * (1 - half)) * 2, (unsigned)(32 * b + 8 * qq) * 2,
+            0);
+      }
+    }
+    __syncthreads();  // the next row block rewrites LDS
+  }
+}
+
+// Dim 512 (SD = 32): four row tiles of operand rows and their tables fill the 160 KB of LDS, so
+// this form stores each 32-column block straight from the accumulators (16-byte pieces of
+// 32 rows after a v_permlane32_swap) instead of through staging areas, one block per wave at a
+// time; every column of the padded projection is computed and written.
+template <int SD>
+__global__ __launch_bounds__(kWaves * 64, 1) void qkv_direct_kernel(QkvParams p) {
+  constexpr int kRows = 128;
   constexpr int kX = kRows * SD * 16 * 2;      // operand fragments
   // Per row: 16 chunks of (cos, sin) for two rotary pairs, chunk c at position c ^ (row & 15)
   // (rows 256 bytes apart would otherwise put one column's reads of 32 rows in one bank).
@@ -168,8 +396,20 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
 }
 
 template <int SD>
-hipError_t launch_t(const QkvParams& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((qkv_kernel<SD>), dim3(grid), dim3(kWaves * 64), 0, stream, p);
+hipError_t launch_direct(const QkvParams& p, hipStream_t stream) {
+  const int cus = device_cus();
+  const int blocks = (p.rows + 127) / 128;
+  const int grid = blocks < cus ? blocks : cus;
+  hipLaunchKernelGGL((qkv_direct_kernel<SD>), dim3(grid), dim3(kWaves * 64), 0, stream, p);
+  return hipGetLastError();
+}
+
+template <int SD, int NR = 4>
+hipError_t launch_t(const QkvParams& p, hipStream_t stream) {
+  const int cus = device_cus();
+  const int blocks = (p.rows + 32 * NR - 1) / (32 * NR);
+  const int grid = blocks < cus ? blocks : cus;
+  hipLaunchKernelGGL((qkv_kernel<SD, NR>), dim3(grid), dim3(kWaves * 64), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -182,17 +422,15 @@ bool qkv_supported(int dim, int cols) {
 hipError_t launch_qkv(const QkvParams& p, hipStream_t stream) {
   // The query scaling rides on the rotary epilogue: a table is required (the block always
   // passes one; without it the query columns would come out unscaled).
-  if (!qkv_supported(p.dim, p.cols) || !p.rope || p.tokens <= 0 || p.token_div <= 0)
+  if (!qkv_supported(p.dim, p.cols) || !p.rope || p.tokens <= 0 || p.token_div <= 0 ||
+      p.width <= 0 || p.width % 64 != 0 || 3 * p.width + p.width / 64 > p.cols)
     return hipErrorInvalidValue;
   if (p.rows <= 0) return hipSuccess;
-  const int cus = device_cus();
-  const int blocks = (p.rows + kRows - 1) / kRows;
-  const int grid = blocks < cus ? blocks : cus;
   switch (p.dim) {
-    case 128: return launch_t<8>(p, grid, stream);
-    case 256: return launch_t<16>(p, grid, stream);
-    case 384: return launch_t<24>(p, grid, stream);
-    default: return launch_t<32>(p, grid, stream);
+    case 128: return launch_t<8>(p, stream);
+    case 256: return launch_t<16>(p, stream);
+    case 384: return launch_t<24>(p, stream);
+    default: return launch_direct<32>(p, stream);
   }
 }
 
