@@ -41,8 +41,9 @@ constexpr int kQueries = kWaves * 32;
 template <bool XH>
 constexpr int kChunks = XH ? 4 : 8;
 
-// Byte offset of 16-byte chunk c (0..7) of row r in a tile of 128-byte rows (K: row = key;
-// V^T: row = channel; a wave's queries: row = query). Chunks are XOR-swizzled by (r >> 1) & 7,
+// Byte offset of 16-byte chunk c (0..7) of row r in a tile of 128-byte rows (K: row = key; a
+// wave's queries: row = query; V^T has its own layout below). Chunks are XOR-swizzled by
+// (r >> 1) & 7,
 // so the 16 lanes that one LDS cycle serves (rows r .. r + 15 of a fragment read, two rows per
 // 256-byte bank line) land on 16 different bank groups.
 __device__ __forceinline__ int row_offset(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
@@ -53,16 +54,28 @@ __device__ __forceinline__ int v_position(int k) {
   return (k & 0x33) | ((k & 4) << 1) | ((k & 8) >> 1);
 }
 
-// Byte offset of the dword holding positions pos, pos + 1 (pos even) of V^T row ch.
-__device__ __forceinline__ int v_offset(int ch, int pos) {
-  return row_offset(ch, pos >> 3) + (pos & 7) * 2;
+// Byte offset of 16-byte chunk c of V^T row r (a channel): rows r and r ^ 1 trade places when
+// bit 2 of r is set, and the chunk is XOR-swizzled by (r3, r1 ^ r4, r2 ^ r5). Two rows share a
+// 256-byte line of the 64 banks, so a 16-byte access's bank group is (physical row & 1, chunk):
+// the 16 lanes that one LDS cycle of the fragment reads serves (rows 16m .. 16m + 15, one
+// chunk) and the 32 lanes that one cycle of the staging writes serves (rows 4i + w, i < 16, one
+// dword of one of two chunks per row) both land on distinct bank groups. Rows 32 + r sit 4 KB
+// after row r with chunk bit 2 flipped.
+__device__ __forceinline__ int vt_row_offset(int r, int c) {
+  const int sw = ((r >> 3) & 1) | ((((r >> 1) ^ (r >> 4)) & 1) << 1) | ((((r >> 2) ^ (r >> 5)) & 1) << 2);
+  return (r ^ ((r >> 2) & 1)) * 128 + ((c ^ sw) << 4);
 }
 
-// The value of lane l ^ 16 (the partner in the other row of the same 32-lane half).
-__device__ __forceinline__ unsigned row_partner(unsigned x, bool odd_row) {
-  const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+// Byte offset of the dword holding positions pos, pos + 1 (pos even) of V^T row ch.
+__device__ __forceinline__ int v_offset(int ch, int pos) {
+  return vt_row_offset(ch, pos >> 3) + (pos & 7) * 2;
+}
+
+// The value of lane l ^ 32 (the partner in the other half of the wave).
+__device__ __forceinline__ unsigned half_partner(unsigned x, bool upper) {
+  const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
   const unsigned a = r[0], b = r[1];
-  return odd_row ? a : b;
+  return upper ? a : b;
 }
 
 // Maximum / sum of x over lanes l and l ^ 32 (the two lanes holding one query).
@@ -203,26 +216,29 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
   unsigned ldq4 = (unsigned)(ts * p.ldq * kEsz), ldk4 = (unsigned)(ts * p.ldk * kEsz),
            ldv4 = (unsigned)(ts * p.ldv * kEsz);
 
-  // K / V staging: thread -> key skey of the tile, channels 4 sc .. 4 sc + 3 of K and V (16
-  // threads read one 256-byte fp32 row). Lanes l and l ^ 16 hold keys 2i and 2i + 1: V^T dwords
-  // pair them, so each lane writes two channels of its key pair (even key: 4 sc, 4 sc + 1; odd
-  // key: 4 sc + 2, 4 sc + 3) after trading halves with its partner.
+  // K / V staging: thread -> channels 4 sc .. 4 sc + 3 of K row skey and of V row vkey (16
+  // threads read one 256-byte fp32 row). A wave's four K rows are tid / 16 in order; its four V
+  // rows the same with bits 0 and 1 of tid / 16 swapped, so that lanes l and l ^ 32 hold keys 2i
+  // and 2i + 1: V^T dwords pair them, and each lane writes two channels of its key pair (even
+  // key: 4 sc, 4 sc + 1; odd key: 4 sc + 2, 4 sc + 3) after trading halves with its partner.
+  // A write instruction's 32 lanes then cover both key pairs of the wave.
   float4 kx = {}, kc = {}, ks = {}, vx = {};
   u32x2 kh = {}, vh = {};
   // parts: 0 = K / V and the key table rows, 1 = K / V only, 2 = the table rows only.
   auto load_tile = [&](const unsigned char* kbase, const unsigned char* vbase, int key0,
                        int parts) {
     const int skey = tid_o >> 4, sc = tid_o & 15;
+    const int vkey = (skey & ~3) | ((skey & 1) << 1) | ((skey >> 1) & 1);
     const unsigned rows = (unsigned)(T - key0);
     if (parts != 2) {
       const rsrc_t kr = make_rsrc(kbase + (long)key0 * ldk4, (rows - 1) * ldk4 + kRowBytes);
       const rsrc_t vr = make_rsrc(vbase + (long)key0 * ldv4, (rows - 1) * ldv4 + kRowBytes);
       if constexpr (XH) {
         kh = __builtin_amdgcn_raw_buffer_load_b64(kr, (unsigned)skey * ldk4 + sc * 8, 0, 0);
-        vh = __builtin_amdgcn_raw_buffer_load_b64(vr, (unsigned)skey * ldv4 + sc * 8, 0, 0);
+        vh = __builtin_amdgcn_raw_buffer_load_b64(vr, (unsigned)vkey * ldv4 + sc * 8, 0, 0);
       } else {
         kx = bload4<ALIGNED>(kr, (unsigned)skey * ldk4 + sc * 16);
-        vx = bload4<ALIGNED>(vr, (unsigned)skey * ldv4 + sc * 16);
+        vx = bload4<ALIGNED>(vr, (unsigned)vkey * ldv4 + sc * 16);
       }
     }
     if constexpr (ROPE && !XH) {
@@ -237,8 +253,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
   };
   auto store_tile = [&](int buf) {
     const int skey = tid_o >> 4, sc = tid_o & 15;
-    const bool odd = (skey & 1) != 0;
-    const int vch = 4 * sc + 2 * (int)odd, vpos = v_position(skey & ~1);
+    const int vkey = (skey & ~3) | ((skey & 1) << 1) | ((skey >> 1) & 1);
+    const bool odd = (vkey & 1) != 0;
+    const int vch = 4 * sc + 2 * (int)odd, vpos = v_position(vkey & ~1);
     u32x2 kw = kh, vw = vh;
     if constexpr (!XH) {
       float4 x = kx;
@@ -249,7 +266,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
     *reinterpret_cast<u32x2*>(lds_k[buf] + row_offset(skey, sc >> 1) + ((sc & 1) << 3)) = kw;
     // Even key: (mine, partner's) of channels 4 sc, 4 sc + 1 (the partner sends its first
     // dword); odd key: (partner's, mine) of 4 sc + 2, 4 sc + 3 (the partner sends its second).
-    const unsigned other = row_partner(odd ? vw[0] : vw[1], odd);
+    const unsigned other = half_partner(odd ? vw[0] : vw[1], odd);
     const unsigned lo = odd ? other : vw[0], hi = odd ? vw[1] : other;
     unsigned char* V = lds_v[buf];
     *reinterpret_cast<unsigned*>(V + v_offset(vch, vpos)) =
@@ -412,10 +429,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
     // reads see the rows staged before, and precede this pass's prefetch into the same rows.
     // Per-lane LDS offsets: K fragment (kb, ds) = keys 32 kb + (l % 32), chunk 2 ds + l / 32;
     // V^T fragment (db, kb, k2) = channel 32 db + (l % 32), chunk 4 kb + 2 k2 + l / 32. Both are
-    // chunk 2 i + l / 32 of row l % 32 (i = ds, or 2 kb + k2), plus 4096 per 32 rows.
-    int fq[4];
+    // chunk 2 i + l / 32 of row l % 32 (i = ds, or 2 kb + k2), plus 4096 per 32 rows (in the V^T
+    // layout, chunk 2 (i ^ 2) + l / 32 of the row 32 below).
+    int fq[4], fv[4];
 #pragma unroll
-    for (int i = 0; i < 4; i++) fq[i] = row_offset(col, 2 * i + half);
+    for (int i = 0; i < 4; i++) {
+      fq[i] = row_offset(col, 2 * i + half);
+      fv[i] = vt_row_offset(col, 2 * i + half);
+    }
     u32x4 qf[4];
     if (active) {
 #pragma unroll
@@ -489,7 +510,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
       for (int k2 = 0; k2 < 2; k2++)
 #pragma unroll
         for (int db = 0; db < 2; db++)
-          o[db] = mfma32(lds16(V + db * 4096 + fq[2 * kb + k2]), pf[k2], o[db]);
+          o[db] = mfma32(lds16(V + db * 4096 + fv[(2 * kb + k2) ^ (2 * db)]), pf[k2], o[db]);
     };
 
     for (int j = 0; j + 1 < ntiles; j++) {

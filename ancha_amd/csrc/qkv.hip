@@ -45,7 +45,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kX + kT];
   float* const cs = reinterpret_cast<float*>(lds + kX);
   // Per wave: one row tile of a pair's output, 32 rows x 128 bytes, 16-byte chunk c of row r at
-  // position c ^ (r & 7), so a wave's stores leave as whole 128-byte lines (8 rows per store).
+  // position c ^ ((r >> 1) & 7), so a wave's stores leave as whole 128-byte lines (8 rows per
+  // store). Two rows share a 256-byte line of the 64 banks: with that swizzle the 16 chunks of
+  // two rows that one LDS cycle of the 16-byte reads serves fall on 16 bank groups, and with the
+  // two 8-byte halves of every chunk swapped in rows 16-31 the 32 lanes (rows) that one cycle of
+  // the 8-byte accumulator writes serves cover all 64 banks.
   __shared__ __attribute__((aligned(16))) unsigned char stage[kWaves][32 * 128];
 
   const int tid = threadIdx.x, lane = tid & 63;
@@ -98,9 +102,9 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
 
   // Pairs of this wave: wave + 8 n (n < mine); pair index % 4 = wave % 4 = its SIMD.
   const int mine = pairs > wave ? (pairs - wave + kWaves - 1) / kWaves : 0;
-  // k steps of weight fragments in flight (two fragments each); with four row tiles, four steps
-  // and the staging epilogue no longer fit the 256 registers of two waves per SIMD
-  constexpr int PD = 2;
+  // k steps of weight fragments in flight (two fragments each): four at dim 384 (255 registers,
+  // QKV 156 -> 150 us at 96 120 rows against two), two at dims 128 and 256.
+  constexpr int PD = SD % 4 == 0 && SD > 16 ? 4 : 2;
   static_assert(SD % PD == 0 && SD >= PD, "K steps come in groups of PD");
 
   for (int blk = blockIdx.x; blk * kRows < p.rows; blk += gridDim.x) {
@@ -185,15 +189,17 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
             tile_values(acc[x][j], 2 * pr + x, j, bias[x], packed);
 #pragma unroll
             for (int q = 0; q < 4; q++)
-              *reinterpret_cast<u32x2*>(st + col * 128 + (((4 * x + q) ^ (col & 7)) << 4) +
-                                        8 * half) = packed[q];
+              *reinterpret_cast<u32x2*>(st + col * 128 + (((4 * x + q) ^ ((col >> 1) & 7)) << 4) +
+                                        8 * (half ^ (col >> 4))) = packed[q];
           }
-          // Rows 8 k + l / 8 of the tile, 16-byte chunk l % 8: whole 128-byte lines.
+          // Rows 8 k + l / 8 of the tile, 16-byte chunk l % 8: whole 128-byte lines. Rows 16-31
+          // (k = 2, 3) hold their chunks' 8-byte halves swapped.
 #pragma unroll
           for (int k = 0; k < 4; k++) {
             const int rr = 8 * k + (lane >> 3);
-            const u32x4 w = *reinterpret_cast<const u32x4*>(
-                st + rr * 128 + (((lane & 7) ^ (rr & 7)) << 4));
+            u32x4 w = *reinterpret_cast<const u32x4*>(
+                st + rr * 128 + (((lane & 7) ^ ((rr >> 1) & 7)) << 4));
+            if (k >= 2) w = u32x4{w[2], w[3], w[0], w[1]};
             __builtin_amdgcn_raw_buffer_store_b128(
                 w, outr, ((unsigned)(32 * j + rr) * p.cols + 8 * (lane & 7)) * 2,
                 (unsigned)(64 * pr) * 2, kStream);
