@@ -48,38 +48,65 @@ __device__ __forceinline__ unsigned v_pair(u32x2 a, u32x2 b, int j) {
   return __builtin_amdgcn_perm(b[j >> 1], a[j >> 1], (j & 1) ? 0x07060302u : 0x05040100u);
 }
 
-// 1/l and sigmoid(gate) scaling and store of one lane's 16 channels (grp*4 + 16*db) of query t.
-// HALF: 1 = fp16 gate and output, 0 = fp32 gate and output, -1 = as o.gate_half / o.half say
-// (a branch the compiler's wait counting cannot see through).
-template <bool GATED, bool ALIGNED, int CP = 0, int HALF = -1>
-__device__ __forceinline__ void store_output(const OutRows& o, const f32x4 (&acc)[4], float l,
-                                             int t, int grp) {
+// fp32 output of one wave's 16 queries q0 .. q0 + 15 as whole 256-byte rows: the lanes' values
+// (1/l and the gate applied) go through the wave's 4 KB LDS area W (row r = query, 16-byte chunk
+// c of row r at position c ^ r, conflict-free for the 16-lane cycles of both passes), then 16
+// lanes store one row per instruction, i.e. whole 128-byte lines (non-temporal stores of
+// 64-byte pieces reach HBM partly as partial lines).
+template <bool GATED, bool ALIGNED, int CP>
+__device__ __forceinline__ void store_output_rows(const OutRows& o, const f32x4 (&acc)[4], float l,
+                                                  int q0, int col, int grp, int lane,
+                                                  unsigned char* W) {
   float scale = 1.0f / l;
-  const bool gate_half = HALF < 0 ? o.gate_half : HALF > 0;
-  const bool out_half = HALF < 0 ? o.half : HALF > 0;
   if constexpr (GATED) {
+    const unsigned t = (unsigned)(q0 + col);
     const float gl =
-        gate_half ? (float)__builtin_bit_cast(
-                          _Float16, __builtin_amdgcn_raw_buffer_load_b16(o.gate, (unsigned)t * o.ldg4, 0, 0))
-                    : bload1(o.gate, (unsigned)t * o.ldg4);
+        o.gate_half ? (float)__builtin_bit_cast(
+                          _Float16, __builtin_amdgcn_raw_buffer_load_b16(o.gate, t * o.ldg4, 0, 0))
+                    : bload1(o.gate, t * o.ldg4);
     scale = scale / (1.0f + expf(-gl));
   }
-  if (out_half) {
-    const unsigned base = (unsigned)t * o.ld4 + grp * 8;
-#pragma unroll
-    for (int db = 0; db < 4; db++) {
-      const u32x2 h = {pack_h2(acc[db][0] * scale, acc[db][1] * scale),
-                       pack_h2(acc[db][2] * scale, acc[db][3] * scale)};
-      __builtin_amdgcn_raw_buffer_store_b64(h, o.out, base + db * 32, 0, CP);
-    }
-    return;
-  }
-  const unsigned base = (unsigned)t * o.ld4 + grp * 16;
 #pragma unroll
   for (int db = 0; db < 4; db++)
-    bstore4<ALIGNED, CP>(o.out, base + db * 64,
-                     make_float4(acc[db][0] * scale, acc[db][1] * scale, acc[db][2] * scale,
-                                 acc[db][3] * scale));
+    *reinterpret_cast<f32x4*>(W + col * 256 + (((grp + 4 * db) ^ col) << 4)) = acc[db] * scale;
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const int r = 4 * k + (lane >> 4), c = lane & 15;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(W + r * 256 + ((c ^ r) << 4));
+    bstore4<ALIGNED, CP>(o.out, (unsigned)(q0 + r) * o.ld4 + c * 16,
+                         make_float4(v[0], v[1], v[2], v[3]));
+  }
+}
+
+// The same for fp16 output (the block's packed projection): 128-byte rows, 8 lanes a row, staged
+// in the wave's own 2 KB of query rows (read into registers before; chunk c of row r at position
+// c ^ ((r >> 1) & 7), conflict-free for the 8-byte writes and the 16-byte reads).
+template <bool GATED, int CP>
+__device__ __forceinline__ void store_output_rows_h(const OutRows& o, const f32x4 (&acc)[4], float l,
+                                                    int q0, int col, int grp, int lane,
+                                                    unsigned char* W) {
+  float scale = 1.0f / l;
+  if constexpr (GATED) {
+    const unsigned t = (unsigned)(q0 + col);
+    const float gl =
+        o.gate_half ? (float)__builtin_bit_cast(
+                          _Float16, __builtin_amdgcn_raw_buffer_load_b16(o.gate, t * o.ldg4, 0, 0))
+                    : bload1(o.gate, t * o.ldg4);
+    scale = scale / (1.0f + expf(-gl));
+  }
+#pragma unroll
+  for (int db = 0; db < 4; db++) {
+    const int chunk = 2 * db + (grp >> 1);
+    *reinterpret_cast<u32x2*>(W + col * 128 + ((chunk ^ ((col >> 1) & 7)) << 4) + 8 * (grp & 1)) =
+        u32x2{pack_h2(acc[db][0] * scale, acc[db][1] * scale),
+              pack_h2(acc[db][2] * scale, acc[db][3] * scale)};
+  }
+#pragma unroll
+  for (int k = 0; k < 2; k++) {
+    const int r = 8 * k + (lane >> 3), c = lane & 7;
+    const u32x4 v = *reinterpret_cast<const u32x4*>(W + r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+    __builtin_amdgcn_raw_buffer_store_b128(v, o.out, (unsigned)(q0 + r) * o.ld4 + c * 16, 0, CP);
+  }
 }
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
@@ -136,6 +163,8 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   __shared__ __attribute__((aligned(16))) unsigned char lds_q[64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_k[64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_v[64 * 128];
+  // The walk (fp32 output): each wave's output rows on their way to whole-row stores.
+  __shared__ __attribute__((aligned(16))) unsigned char lds_o[kWalk ? 4 : 1][kWalk ? 4096 : 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
@@ -279,11 +308,14 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
             *reinterpret_cast<const u32x4*>(lds_v + v_base[ks][db & 1] + db * 2048), pf[ks], o[db]);
       lsum = mfma16x16x32(ones, pf[ks], lsum);
     }
-    // fp16 input stores fp16 (fixed at compile time: no branch between the loads and the
-    // waits, 1.5 % off the layer). The fp32 walk keeps the run-time form: with the branch
-    // removed the compiler's wait placement changes and the walk measured 5 % slower.
-    store_output<GATED, ALIGNED, kStream, XH ? 1 : -1>(out_rows(p, g, h), o, lsum[0], q0 + col,
-                                                       grp);
+    // Whole output rows per store: the fp32 walk (fp32 in and out) through the wave's LDS
+    // area, fp16 input (fp16 out) through the wave's own query rows.
+    if constexpr (kWalk)
+      store_output_rows<GATED, ALIGNED, kStream>(out_rows(p, g, h), o, lsum[0], q0, col, grp, lane,
+                                                 lds_o[wave]);
+    else
+      store_output_rows_h<GATED, kStream>(out_rows(p, g, h), o, lsum[0], q0, col, grp, lane,
+                                          lds_q + wave * 2048);
   };
 
   if constexpr (kWalk) {
