@@ -142,9 +142,10 @@ __device__ __forceinline__ f32x16 zero16() {
 }
 
 // LDS-direct buffer load: each lane's 16 bytes at `off` land at dst + 16 * lane.
+template <int CP = 0>
 __device__ __forceinline__ void load_lds16(rsrc_t r, unsigned char* dst, unsigned off) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)dst, 16,
-                                           off, 0, 0, 0);
+                                           off, 0, 0, CP);
 }
 
 // The same with 4 bytes per lane: lane l's dword at `off` lands at dst + 4 * l.
@@ -323,12 +324,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
       // row 8 c + l / 8, stored chunk l % 8 = logical chunk (l % 8) ^ ((row >> 1) & 7).
       const int r = 8 * c + (lane >> 3);
       const int cc = (lane & 7) ^ ((r >> 1) & 7);
-      load_lds16(qr, lds_q[wave] + 1024 * c, (unsigned)r * ldq4 + cc * 16);
+      load_lds16<kStream>(qr, lds_q[wave] + 1024 * c, (unsigned)r * ldq4 + cc * 16);
     } else if constexpr (ALIGNED) {
       // Rows 4 c + l / 16, 16-byte piece l % 16: query row, then cos and sin table rows.
       const int r = 4 * c + (lane >> 4), cc = lane & 15;
       unsigned char* R = lds_raw[wave];
-      load_lds16(qr, R, (unsigned)r * ldq4 + cc * 16);
+      load_lds16<kStream>(qr, R, (unsigned)r * ldq4 + cc * 16);
       if constexpr (ROPE) {
         const unsigned rows = (unsigned)(T - q0);
         const rsrc_t cr = make_rsrc(p.rope + (long)q0 * 64, rows * 256);
