@@ -156,17 +156,23 @@ struct BandRaw<true> {
   u32x2 v[4];
 };
 
-template <bool GATED, bool ROPE, bool ALIGNED, bool XH>
-__global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int problems) {
+// PK: problems side by side in one workgroup (PK x 4 waves): the heads h0 .. h0 + PK - 1 of one
+// group, whose rows are one contiguous PK x 256-byte piece of each token row (fp32 walk).
+template <bool GATED, bool ROPE, bool ALIGNED, bool XH, int PK = 1>
+__global__ __launch_bounds__(256 * PK) void attention_band_kernel(AttnParams p, int items) {
   static_assert(!(XH && ROPE), "fp16 input arrives rotated");
+  static_assert(PK == 1 || (PK == 2 && !XH), "side by side: the fp32 walk");
   constexpr bool kWalk = !XH;
-  __shared__ __attribute__((aligned(16))) unsigned char lds_q[64 * 128];
-  __shared__ __attribute__((aligned(16))) unsigned char lds_k[64 * 128];
-  __shared__ __attribute__((aligned(16))) unsigned char lds_v[64 * 128];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_q[PK][64 * 128];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_k[PK][64 * 128];
+  __shared__ __attribute__((aligned(16))) unsigned char lds_v[PK][64 * 128];
   // The walk (fp32 output): each wave's output rows on their way to whole-row stores.
-  __shared__ __attribute__((aligned(16))) unsigned char lds_o[kWalk ? 4 : 1][kWalk ? 4096 : 16];
+  __shared__ __attribute__((aligned(16)))
+  unsigned char lds_o[kWalk ? 4 * PK : 1][kWalk ? 4096 : 16];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Problem slot of this wave (its head h0 + ps) and its wave index within the slot.
+  const int ps = PK > 1 ? wave >> 2 : 0, w4 = wave & 3;
   const int col = lane & 15, grp = lane >> 4;
   const int T = p.tokens;
   const long ts = p.tstep;
@@ -174,10 +180,12 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   const unsigned ldq4 = (unsigned)(ts * p.ldq * kEsz), ldk4 = (unsigned)(ts * p.ldk * kEsz),
                  ldv4 = (unsigned)(ts * p.ldv * kEsz);
 
-  // Staging roles: q / k rows srow + 16*it at channels 4*sc; v key pairs (2*(srow + 16*it),
-  // +1), it < 2. fp16 input: q / k rows (tid >> 3) + 32*it as 16-byte chunks tid & 7, v key
-  // pairs at 8-byte channel groups sc. Rows at or past T read as 0.
-  const int srow = tid >> 4, sc = tid & 15;
+  // Staging roles: q / k rows srow + 16*it at channels 4*sc of head slot hs; v key pairs
+  // (2*(srow + 16*it), +1), it < 2 (32 threads a row of PK = 2 heads). fp16 input: q / k rows
+  // (tid >> 3) + 32*it as 16-byte chunks tid & 7, v key pairs at 8-byte channel groups sc. Rows
+  // at or past T read as 0.
+  const int srow = PK > 1 ? tid >> 5 : tid >> 4, sc = tid & 15;
+  const int hs = PK > 1 ? (tid >> 4) & 1 : 0;
   // This thread's rotary table values (query cos / sin, key cos / sin of its four rows).
   float4 tab[4][4];
   if constexpr (ROPE) {
@@ -190,10 +198,14 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   }
   auto load = [&](int g, int h, BandRaw<XH>& r) {
     const long row0 = group_row(p, g);
+    // The descriptor's base is wave-uniform (head h); a thread's head slot hs is a 256-byte
+    // offset in its vector offset, which the range check covers (rows at or past T read 0: the
+    // row stride is at least PK heads).
     auto rows_of = [&](const float* base, long ld, unsigned ld4) {
       return make_rsrc(reinterpret_cast<const unsigned char*>(base) + (row0 * ld + h * 64) * kEsz,
-                       (unsigned)(T - 1) * ld4 + kRowBytes);
+                       (unsigned)(T - 1) * ld4 + PK * kRowBytes);
     };
+    const unsigned hoff = (unsigned)hs * kRowBytes;
     const rsrc_t qr = rows_of(p.q, p.ldq, ldq4);
     const rsrc_t kr = rows_of(p.k, p.ldk, ldk4);
     const rsrc_t vr = rows_of(p.v, p.ldv, ldv4);
@@ -214,15 +226,15 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
 #pragma unroll
       for (int it = 0; it < 4; it++) {
         const unsigned rr = (unsigned)(srow + 16 * it);
-        r.q[it] = bload4<ALIGNED, kStream>(qr, rr * ldq4 + sc * 16);
-        r.k[it] = bload4<ALIGNED, kStream>(kr, rr * ldk4 + sc * 16);
+        r.q[it] = bload4<ALIGNED, kStream>(qr, rr * ldq4 + hoff + sc * 16);
+        r.k[it] = bload4<ALIGNED, kStream>(kr, rr * ldk4 + hoff + sc * 16);
       }
 #pragma unroll
       for (int it = 0; it < 2; it++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
-          r.v[it * 2 + j] =
-              bload4<ALIGNED, kStream>(vr, (unsigned)(2 * (srow + 16 * it) + j) * ldv4 + sc * 16);
+          r.v[it * 2 + j] = bload4<ALIGNED, kStream>(
+              vr, (unsigned)(2 * (srow + 16 * it) + j) * ldv4 + hoff + sc * 16);
     }
   };
   auto stage = [&](const BandRaw<XH>& r) {
@@ -230,14 +242,14 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
 #pragma unroll
       for (int it = 0; it < 2; it++) {
         const int off = k_offset((tid >> 3) + 32 * it, tid & 7);
-        *reinterpret_cast<u32x4*>(lds_q + off) = r.q[it];
-        *reinterpret_cast<u32x4*>(lds_k + off) = r.k[it];
+        *reinterpret_cast<u32x4*>(lds_q[0] + off) = r.q[it];
+        *reinterpret_cast<u32x4*>(lds_k[0] + off) = r.k[it];
       }
 #pragma unroll
       for (int it = 0; it < 2; it++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
-          *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+          *reinterpret_cast<unsigned*>(lds_v[0] + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
               v_pair(r.v[it * 2], r.v[it * 2 + 1], j);
     } else {
 #pragma unroll
@@ -250,34 +262,34 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
         }
         q = scale4(q, kLog2e);
         const int off = k_offset(rr, sc >> 1) + ((sc & 1) << 3);
-        *reinterpret_cast<u32x2*>(lds_q + off) = u32x2{pack_h2(q.x, q.y), pack_h2(q.z, q.w)};
-        *reinterpret_cast<u32x2*>(lds_k + off) = u32x2{pack_h2(k.x, k.y), pack_h2(k.z, k.w)};
+        *reinterpret_cast<u32x2*>(lds_q[hs] + off) = u32x2{pack_h2(q.x, q.y), pack_h2(q.z, q.w)};
+        *reinterpret_cast<u32x2*>(lds_k[hs] + off) = u32x2{pack_h2(k.x, k.y), pack_h2(k.z, k.w)};
       }
 #pragma unroll
       for (int it = 0; it < 2; it++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
-          *reinterpret_cast<unsigned*>(lds_v + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+          *reinterpret_cast<unsigned*>(lds_v[hs] + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
               pack_h2(comp(r.v[it * 2], j), comp(r.v[it * 2 + 1], j));
     }
   };
 
-  const int q0 = wave * 16;
+  const int q0 = w4 * 16;
   const int kq_base[2] = {k_offset(col, grp), k_offset(col, 4 + grp)};
   const int vsw = (col ^ (col >> 2)) & 7;
   const int v_base[2][2] = {{col * 128 + ((grp ^ vsw) << 4), col * 128 + ((grp ^ vsw ^ 4) << 4)},
                             {col * 128 + (((4 + grp) ^ vsw) << 4),
                              col * 128 + (((4 + grp) ^ vsw ^ 4) << 4)}};
   auto compute = [&](int g, int h) {
-    const u32x4 qf[2] = {*reinterpret_cast<const u32x4*>(lds_q + kq_base[0] + wave * 2048),
-                         *reinterpret_cast<const u32x4*>(lds_q + kq_base[1] + wave * 2048)};
+    const u32x4 qf[2] = {*reinterpret_cast<const u32x4*>(lds_q[ps] + kq_base[0] + w4 * 2048),
+                         *reinterpret_cast<const u32x4*>(lds_q[ps] + kq_base[1] + w4 * 2048)};
     f32x4 s[4];
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) {
       s[kb] = zero4();
 #pragma unroll
       for (int ds = 0; ds < 2; ds++)
-        s[kb] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_k + kq_base[ds] + kb * 2048),
+        s[kb] = mfma16x16x32(*reinterpret_cast<const u32x4*>(lds_k[ps] + kq_base[ds] + kb * 2048),
                              qf[ds], s[kb]);
     }
     if (T < 64) {
@@ -305,17 +317,18 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
 #pragma unroll
       for (int db = 0; db < 4; db++)
         o[db] = mfma16x16x32(
-            *reinterpret_cast<const u32x4*>(lds_v + v_base[ks][db & 1] + db * 2048), pf[ks], o[db]);
+            *reinterpret_cast<const u32x4*>(lds_v[ps] + v_base[ks][db & 1] + db * 2048), pf[ks],
+            o[db]);
       lsum = mfma16x16x32(ones, pf[ks], lsum);
     }
     // Whole output rows per store: the fp32 walk (fp32 in and out) through the wave's LDS
     // area, fp16 input (fp16 out) through the wave's own query rows.
     if constexpr (kWalk)
-      store_output_rows<GATED, ALIGNED, kStream>(out_rows(p, g, h), o, lsum[0], q0, col, grp, lane,
-                                                 lds_o[wave]);
+      store_output_rows<GATED, ALIGNED, kStream>(out_rows(p, g, h + ps), o, lsum[0], q0, col, grp,
+                                                 lane, lds_o[wave]);
     else
       store_output_rows_h<GATED, kStream>(out_rows(p, g, h), o, lsum[0], q0, col, grp, lane,
-                                          lds_q + wave * 2048);
+                                          lds_q[0] + wave * 2048);
   };
 
   if constexpr (kWalk) {
@@ -326,28 +339,30 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
     // anyway (its q rows are zero; rows at or past T lie outside the output's buffer range, so
     // their stores are dropped): no branch around the loads and stores keeps the wait counts
     // fixed.
-    auto step = [&](int prob, const BandRaw<XH>& cur, BandRaw<XH>& nxt) {
+    // Item b: group b / (heads / PK), heads PK * (b % (heads / PK)) + 0 .. PK - 1.
+    const int hpg = p.heads / PK;
+    auto step = [&](int item, const BandRaw<XH>& cur, BandRaw<XH>& nxt) {
       stage(cur);
       __syncthreads();
-      const int next = min(prob + (int)gridDim.x, problems - 1);
-      load(next / p.heads, next % p.heads, nxt);
-      compute(prob / p.heads, prob % p.heads);
+      const int next = min(item + (int)gridDim.x, items - 1);
+      load(next / hpg, PK * (next % hpg), nxt);
+      compute(item / hpg, PK * (item % hpg));
       __syncthreads();  // the next step restages LDS
     };
     // The first step is peeled so the loop is entered with the same loads and stores
     // outstanding as each turn ends with (else the wait counts at the loop head are merged down
     // to a full drain).
     BandRaw<XH> a, b;
-    int prob = blockIdx.x;
-    load(prob / p.heads, prob % p.heads, a);
-    step(prob, a, b);
+    int item = blockIdx.x;
+    load(item / hpg, PK * (item % hpg), a);
+    step(item, a, b);
     while (true) {
-      prob += gridDim.x;
-      if (prob >= problems) break;
-      step(prob, b, a);
-      prob += gridDim.x;
-      if (prob >= problems) break;
-      step(prob, a, b);
+      item += gridDim.x;
+      if (item >= items) break;
+      step(item, b, a);
+      item += gridDim.x;
+      if (item >= items) break;
+      step(item, a, b);
     }
   } else {
     int g, h;
@@ -360,28 +375,37 @@ __global__ __launch_bounds__(256) void attention_band_kernel(AttnParams p, int p
   }
 }
 
+// The fp32 walk: as many workgroups of 256 * PK threads as the CUs hold at once.
+template <bool GATED, bool ROPE, bool ALIGNED, int PK>
+static hipError_t launch_band_walk(const AttnParams& p, hipStream_t stream) {
+  auto kernel = attention_band_kernel<GATED, ROPE, ALIGNED, false, PK>;
+  const int items = p.groups * (p.heads / PK);
+  static int per_cu = 0;
+  if (per_cu <= 0 &&
+      (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256 * PK, 0) != hipSuccess ||
+       per_cu <= 0))
+    per_cu = 2 / PK;
+  const long cap = (long)per_cu * device_cus();
+  const int grid = cap < items ? (int)cap : items;
+  hipLaunchKernelGGL(kernel, dim3(grid), dim3(256 * PK), 0, stream, p, items);
+  return hipGetLastError();
+}
+
 template <bool GATED, bool ROPE, bool ALIGNED, bool XH = false>
 static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
   const int T = p.tokens;
-  if (T <= 64) {
-    auto kernel = attention_band_kernel<GATED, ROPE, ALIGNED, XH>;
-    const int problems = p.groups * p.heads;
-    int grid = problems;
-    if constexpr (!XH) {
-      // The walk: as many workgroups as the CUs hold at once.
-      static int per_cu = 0;
-      if (per_cu <= 0 &&
-          (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 256, 0) != hipSuccess ||
-           per_cu <= 0))
-        per_cu = 2;
-      const long cap = (long)per_cu * device_cus();
-      if (cap < problems) grid = (int)cap;
-    }
-    hipLaunchKernelGGL(kernel, dim3(grid), dim3(256), 0, stream, p, problems);
+  if (T > 64) return launch_attention_long(p, GATED, ROPE, ALIGNED, stream);
+  if constexpr (!XH) {
+    // Two heads side by side where the head count is even (each token row's two head slices
+    // are one contiguous 512-byte piece), one problem per slot otherwise.
+    if (p.heads % 2 == 0) return launch_band_walk<GATED, ROPE, ALIGNED, 2>(p, stream);
+    return launch_band_walk<GATED, ROPE, ALIGNED, 1>(p, stream);
   } else {
-    return launch_attention_long(p, GATED, ROPE, ALIGNED, stream);
+    const int problems = p.groups * p.heads;
+    hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED, XH>), dim3(problems), dim3(256),
+                       0, stream, p, problems);
+    return hipGetLastError();
   }
-  return hipGetLastError();
 }
 
 bool attention_grid_fits(size_t groups, size_t tokens, size_t heads) {
