@@ -161,7 +161,7 @@ struct BandRaw<true> {
 template <bool GATED, bool ROPE, bool ALIGNED, bool XH, int PK = 1>
 __global__ __launch_bounds__(256 * PK) void attention_band_kernel(AttnParams p, int items) {
   static_assert(!(XH && ROPE), "fp16 input arrives rotated");
-  static_assert(PK == 1 || (PK == 2 && !XH), "side by side: the fp32 walk");
+  static_assert(PK == 1 || PK == 2, "one or two heads side by side");
   constexpr bool kWalk = !XH;
   __shared__ __attribute__((aligned(16))) unsigned char lds_q[PK][64 * 128];
   __shared__ __attribute__((aligned(16))) unsigned char lds_k[PK][64 * 128];
@@ -182,10 +182,12 @@ __global__ __launch_bounds__(256 * PK) void attention_band_kernel(AttnParams p, 
 
   // Staging roles: q / k rows srow + 16*it at channels 4*sc of head slot hs; v key pairs
   // (2*(srow + 16*it), +1), it < 2 (32 threads a row of PK = 2 heads). fp16 input: q / k rows
-  // (tid >> 3) + 32*it as 16-byte chunks tid & 7, v key pairs at 8-byte channel groups sc. Rows
-  // at or past T read as 0.
+  // xrow + 32*it as 16-byte chunks xc of head slot xhs (16 threads a row of 2 heads), v key pairs
+  // at 8-byte channel groups sc of head slot hs. Rows at or past T read as 0.
   const int srow = PK > 1 ? tid >> 5 : tid >> 4, sc = tid & 15;
   const int hs = PK > 1 ? (tid >> 4) & 1 : 0;
+  const int xrow = PK > 1 ? tid >> 4 : tid >> 3, xc = tid & 7;
+  const int xhs = PK > 1 ? (tid >> 3) & 1 : 0;
   // This thread's rotary table values (query cos / sin, key cos / sin of its four rows).
   float4 tab[4][4];
   if constexpr (ROPE) {
@@ -205,23 +207,25 @@ __global__ __launch_bounds__(256 * PK) void attention_band_kernel(AttnParams p, 
       return make_rsrc(reinterpret_cast<const unsigned char*>(base) + (row0 * ld + h * 64) * kEsz,
                        (unsigned)(T - 1) * ld4 + PK * kRowBytes);
     };
-    const unsigned hoff = (unsigned)hs * kRowBytes;
+    const unsigned hoff = (unsigned)hs * kRowBytes, xhoff = (unsigned)xhs * kRowBytes;
     const rsrc_t qr = rows_of(p.q, p.ldq, ldq4);
     const rsrc_t kr = rows_of(p.k, p.ldk, ldk4);
     const rsrc_t vr = rows_of(p.v, p.ldv, ldv4);
     if constexpr (XH) {
 #pragma unroll
       for (int it = 0; it < 2; it++) {
-        const unsigned rr = (unsigned)((tid >> 3) + 32 * it);
-        r.q[it] = __builtin_amdgcn_raw_buffer_load_b128(qr, rr * ldq4 + (tid & 7) * 16, 0, kStream);
-        r.k[it] = __builtin_amdgcn_raw_buffer_load_b128(kr, rr * ldk4 + (tid & 7) * 16, 0, kStream);
+        const unsigned rr = (unsigned)(xrow + 32 * it);
+        r.q[it] =
+            __builtin_amdgcn_raw_buffer_load_b128(qr, rr * ldq4 + xhoff + xc * 16, 0, kStream);
+        r.k[it] =
+            __builtin_amdgcn_raw_buffer_load_b128(kr, rr * ldk4 + xhoff + xc * 16, 0, kStream);
       }
 #pragma unroll
       for (int it = 0; it < 2; it++)
 #pragma unroll
         for (int j = 0; j < 2; j++)
           r.v[it * 2 + j] = __builtin_amdgcn_raw_buffer_load_b64(
-              vr, (unsigned)(2 * (srow + 16 * it) + j) * ldv4 + sc * 8, 0, kStream);
+              vr, (unsigned)(2 * (srow + 16 * it) + j) * ldv4 + hoff + sc * 8, 0, kStream);
     } else {
 #pragma unroll
       for (int it = 0; it < 4; it++) {
@@ -241,15 +245,15 @@ __global__ __launch_bounds__(256 * PK) void attention_band_kernel(AttnParams p, 
     if constexpr (XH) {
 #pragma unroll
       for (int it = 0; it < 2; it++) {
-        const int off = k_offset((tid >> 3) + 32 * it, tid & 7);
-        *reinterpret_cast<u32x4*>(lds_q[0] + off) = r.q[it];
-        *reinterpret_cast<u32x4*>(lds_k[0] + off) = r.k[it];
+        const int off = k_offset(xrow + 32 * it, xc);
+        *reinterpret_cast<u32x4*>(lds_q[xhs] + off) = r.q[it];
+        *reinterpret_cast<u32x4*>(lds_k[xhs] + off) = r.k[it];
       }
 #pragma unroll
       for (int it = 0; it < 2; it++)
 #pragma unroll
         for (int j = 0; j < 4; j++)
-          *reinterpret_cast<unsigned*>(lds_v[0] + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
+          *reinterpret_cast<unsigned*>(lds_v[hs] + vtc_offset(sc * 4 + j, 2 * (srow + 16 * it))) =
               v_pair(r.v[it * 2], r.v[it * 2 + 1], j);
     } else {
 #pragma unroll
@@ -327,8 +331,8 @@ __global__ __launch_bounds__(256 * PK) void attention_band_kernel(AttnParams p, 
       store_output_rows<GATED, ALIGNED, kStream>(out_rows(p, g, h + ps), o, lsum[0], q0, col, grp,
                                                  lane, lds_o[wave]);
     else
-      store_output_rows_h<GATED, kStream>(out_rows(p, g, h), o, lsum[0], q0, col, grp, lane,
-                                          lds_q[0] + wave * 2048);
+      store_output_rows_h<GATED, kStream>(out_rows(p, g, h + ps), o, lsum[0], q0, col, grp, lane,
+                                          lds_q[ps] + w4 * 2048);
   };
 
   if constexpr (kWalk) {
@@ -365,8 +369,10 @@ __global__ __launch_bounds__(256 * PK) void attention_band_kernel(AttnParams p, 
       step(item, a, b);
     }
   } else {
+    // One item per workgroup: group g, heads h .. h + PK - 1 (pairs of heads as units).
     int g, h;
-    band_problem(blockIdx.x, p.groups, p.heads, g, h);
+    band_problem(blockIdx.x, p.groups, p.heads / PK, g, h);
+    h *= PK;
     BandRaw<XH> r;
     load(g, h, r);
     stage(r);
@@ -401,9 +407,16 @@ static hipError_t launch_attention_t(const AttnParams& p, hipStream_t stream) {
     if (p.heads % 2 == 0) return launch_band_walk<GATED, ROPE, ALIGNED, 2>(p, stream);
     return launch_band_walk<GATED, ROPE, ALIGNED, 1>(p, stream);
   } else {
-    const int problems = p.groups * p.heads;
-    hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED, XH>), dim3(problems), dim3(256),
-                       0, stream, p, problems);
+    // One item (one or two heads of a group) per workgroup.
+    if (p.heads % 2 == 0) {
+      const int items = p.groups * (p.heads / 2);
+      hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED, XH, 2>), dim3(items),
+                         dim3(512), 0, stream, p, items);
+    } else {
+      const int items = p.groups * p.heads;
+      hipLaunchKernelGGL((attention_band_kernel<GATED, ROPE, ALIGNED, XH>), dim3(items), dim3(256),
+                         0, stream, p, items);
+    }
     return hipGetLastError();
   }
 }
