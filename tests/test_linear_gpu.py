@@ -303,3 +303,18 @@ def test_block_wide_rows(gpu):
     err = float(np.abs(got - want).max())
     print(f"block dim {dim}: max|diff| {err:.3e}", flush=True)
     assert err < 2e-3
+
+
+@pytest.mark.parametrize("tokens", [60, 130])
+def test_block_odd_head_count(gpu, tokens):
+    """3 heads (inner 192): the attention kernels' one-head items (an odd head count cannot be
+    paired) on the block's packed fp16 projection, band (T <= 64) and long-sequence lengths."""
+    dim, heads, hidden, groups = 128, 3, 512, 2
+    w = _block_weights(dim, heads, hidden, normalized=True)
+    x = W.normal((groups, tokens, dim), 90 + tokens, 1.0)
+    block = roformer.Transformer(w, gpu)
+    got = block(dev(x, gpu), roformer.axis_rope(W.rope_freqs(), tokens, gpu)).cpu().numpy()
+    want = O.transformer_forward(w, x, kernels=True)
+    err = float(np.abs(got - want).max())
+    print(f"block 3 heads, T={tokens}: max|diff| {err:.3e}", flush=True)
+    assert err < 2e-3
