@@ -7,23 +7,23 @@
 // logits, 3 width + width / 64 of them, rounded up to a 32-column block; the packed layout's
 // zero padding after them is never read by the attention kernels and is left as it is.
 //
-// 128 rows per workgroup: their fp16 operand rows sit in LDS for the whole block as B
-// fragments of v_mfma_f32_32x32x16_f16 (straight from HBM with direct-to-LDS loads), with the
+// 128 rows per workgroup (96 at dim 512): their fp16 operand rows sit in LDS for the whole block
+// as B fragments of v_mfma_f32_32x32x16_f16 (straight from HBM with direct-to-LDS loads), with the
 // rows' rotary cos / sin (32 + 32 per row) next to them. The 8 waves walk the output in pairs of
 // 32-column blocks (pair p on SIMD p % 4, so the SIMDs get the same count); per pair a wave
-// accumulates all 128 rows (4 x 32-row MFMA tiles per block) over K, so each operand B fragment
-// read from LDS feeds two MFMAs and each weight A fragment (a contiguous kilobyte of the
-// fragment-major W^T) four. The epilogue takes one 32-row tile of the pair at a time: bias,
+// accumulates all its rows (4 or 3 32-row MFMA tiles per block) over K, so each operand B
+// fragment read from LDS feeds two MFMAs and each weight A fragment (a contiguous kilobyte of the
+// fragment-major W^T) four (three). The epilogue takes one 32-row tile of the pair at a time: bias,
 // rotary and query scale on the accumulators (lane l owns row l % 32, columns 8q + 4(l/32) .. +3
 // of each block: both members of every rotary pair), fp16 into a 4 KB staging area of the wave,
 // read back so that each store covers 8 whole rows of the pair, i.e. whole 128-byte lines,
 // written non-temporally (the projection is read once, by the next kernel). Measured against
 // stores of 32-byte row pieces from the accumulators: the 320 MB output costs ~26 % of the
 // kernel that way, whole lines through the caches save 10 % of it, non-temporal whole lines 17 %.
-// An odd last block is split by row tile over the four waves of the first SIMD slots. No
+// An odd last block is split by row tile over the first four (three) waves. No
 // barriers inside the column walk, so the two waves of a SIMD drift apart and one's epilogue
-// runs beside the other's MFMAs. At dim 512 the operand rows and tables of 128 rows fill the
-// LDS, and qkv_direct_kernel (below) stores from the accumulators instead.
+// runs beside the other's MFMAs. At dim 512 the operand rows, tables and staging areas of 96
+// rows fill 152 KB of the LDS.
 #include "buffer.hpp"
 #include "common.hpp"
 #include "kernels.hpp"
@@ -34,7 +34,7 @@ namespace {
 constexpr int kWaves = 8;
 constexpr int kFrag = 1024;
 
-// SD = dim / 16 k steps (dims 128, 256, 384); NR = 4 32-row tiles per row block.
+// SD = dim / 16 k steps (dims 128 - 512); NR 32-row tiles per row block (4; 3 at dim 512).
 template <int SD, int NR>
 __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
   constexpr int kRows = 32 * NR;
@@ -102,8 +102,8 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
 
   // Pairs of this wave: wave + 8 n (n < mine); pair index % 4 = wave % 4 = its SIMD.
   const int mine = pairs > wave ? (pairs - wave + kWaves - 1) / kWaves : 0;
-  // k steps of weight fragments in flight (two fragments each): four at dim 384 (255 registers,
-  // QKV 156 -> 150 us at 96 120 rows against two), two at dims 128 and 256.
+  // k steps of weight fragments in flight (two fragments each): four at dims 384 (255 registers,
+  // QKV 156 -> 150 us at 96 120 rows against two) and 512, two at dims 128 and 256.
   constexpr int PD = SD % 4 == 0 && SD > 16 ? 4 : 2;
   static_assert(SD % PD == 0 && SD >= PD, "K steps come in groups of PD");
 
@@ -254,162 +254,6 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
   }
 }
 
-// Dim 512 (SD = 32): four row tiles of operand rows and their tables fill the 160 KB of LDS, so
-// this form stores each 32-column block straight from the accumulators (16-byte pieces of
-// 32 rows after a v_permlane32_swap) instead of through staging areas, one block per wave at a
-// time; every column of the padded projection is computed and written.
-template <int SD>
-__global__ __launch_bounds__(kWaves * 64, 1) void qkv_direct_kernel(QkvParams p) {
-  constexpr int kRows = 128;
-  constexpr int kX = kRows * SD * 16 * 2;      // operand fragments
-  // Per row: 16 chunks of (cos, sin) for two rotary pairs, chunk c at position c ^ (row & 15)
-  // (rows 256 bytes apart would otherwise put one column's reads of 32 rows in one bank).
-  constexpr int kT = kRows * 64 * 4;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[kX + kT];
-  float* const cs = reinterpret_cast<float*>(lds + kX);
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = lane >> 5, col = lane & 31;
-  const unsigned lane16 = (unsigned)lane * 16;
-  const int blocks = p.cols / 32;
-  const int dim = SD * 16;
-  const rsrc_t wr = make_rsrc(p.w, (unsigned)(p.cols * dim * 2));
-  const rsrc_t br = make_rsrc(p.bias, (unsigned)(p.cols * 4));
-  const bool rot = p.rope != nullptr;
-  const rsrc_t tr = make_rsrc(rot ? p.rope : p.bias, rot ? (unsigned)(4 * p.tokens * 256) : 0u);
-
-  for (int blk = blockIdx.x; blk * kRows < p.rows; blk += gridDim.x) {
-    const int row0 = blk * kRows;
-    const int nrows = min(kRows, p.rows - row0);
-    const rsrc_t xr = make_rsrc(p.xh + (long)row0 * dim, (unsigned)(nrows * dim * 2));
-    const rsrc_t outr = make_rsrc(p.out + (long)row0 * p.cols, (unsigned)(nrows * p.cols * 2));
-    // Operand rows as B fragments: fragment (jb, s) = rows 32 jb + (l % 32), k 16 s + 8 (l / 32).
-    for (int f = wave; f < 4 * SD; f += kWaves) {
-      const int jb = f / SD, s = f % SD;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          xr, (__attribute__((address_space(3))) void*)(lds + f * kFrag), 16,
-          ((unsigned)(32 * jb + col) * dim + 16 * s + 8 * half) * 2, 0, 0, 0);
-    }
-    // Key-table cos / sin of each row's token (the query tables are these times 1/8).
-    if (rot)
-      for (int e = tid; e < kRows * 32; e += kWaves * 64) {
-        const int r = e >> 5, i = e & 31;
-        const int tok = ((row0 + r) / p.token_div) % p.tokens;
-        float* slot = cs + r * 64 + (((i >> 1) ^ (r & 15)) << 2) + 2 * (i & 1);
-        slot[0] = bload1(tr, (unsigned)((2 * p.tokens + tok) * 64 + 2 * i) * 4);
-        slot[1] = bload1(tr, (unsigned)((3 * p.tokens + tok) * 64 + 2 * i + 1) * 4);
-      }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-
-    constexpr int PD = 8;  // weight fragments in flight
-    static_assert(SD % PD == 0 && SD >= PD, "K steps come in groups of PD");
-    u32x4 a[PD];
-    // The wave's blocks b = wave + 8 n; its A fragments stream through the ring across blocks.
-    const int mine = (blocks - wave + kWaves - 1) / kWaves;
-#pragma unroll
-    for (int i = 0; i < PD; i++)
-      a[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane16, (unsigned)((wave * SD + i) * kFrag),
-                                                   0);
-    for (int n = 0; n < mine; n++) {
-      const int b = wave + kWaves * n;
-      // The operand fragments are the same for every column block; an opaque per-block offset
-      // keeps the compiler from hoisting all their LDS reads (4 * SD fragments) out of the loop.
-      int opaque = 0;
-      asm volatile("" : "+s"(opaque));
-      const unsigned char* X = lds + opaque;
-      f32x16 acc[4];
-#pragma unroll
-      for (int j = 0; j < 4; j++) acc[j] = mfma32_zero();
-      // This block's bias columns (used after the K loop).
-      float4 bias[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++)
-        bias[q] = __builtin_bit_cast(
-            float4, __builtin_amdgcn_raw_buffer_load_b128(br, 16 * half,
-                                                          (unsigned)(32 * b + 8 * q) * 4, 0));
-      // Fragment offsets of this block and of the next one (the last block reloads itself:
-      // unconditional loads keep the ring in fixed registers).
-      const unsigned here = (unsigned)(b * SD * kFrag);
-      const unsigned next = (unsigned)(min(b + kWaves, wave + kWaves * (mine - 1)) * SD * kFrag);
-#pragma unroll
-      for (int s = 0; s < SD; s++) {
-        const u32x4 cur = a[s % PD];
-        a[s % PD] = __builtin_amdgcn_raw_buffer_load_b128(
-            wr, lane16, s + PD < SD ? here + (s + PD) * kFrag : next + (s + PD - SD) * kFrag, 0);
-        // Operand reads and MFMAs of one step; the scheduling barrier keeps the compiler from
-        // pulling later steps' LDS reads forward (all 4 * SD would not fit in registers).
-#pragma unroll
-        for (int j = 0; j < 4; j++)
-          acc[j] = mfma32(cur, *reinterpret_cast<const u32x4*>(X + (j * SD + s) * kFrag + lane16),
-                          acc[j]);
-        if (s % 4 == 3) __builtin_amdgcn_sched_barrier(0);
-      }
-      // Epilogue: bias -> rotary -> query scale (fused/gemm.rs:46-82 order), fp16. Lanes l and
-      // l + 32 then trade halves (v_permlane32_swap) so each holds 8 consecutive columns of its
-      // row: one 16-byte store per lane covers 16 columns of 32 rows.
-      u32x2 packed[4][4];  // [q][j]
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int c = 32 * b + 8 * q + 4 * half;  // this lane's 4 columns c .. c + 3
-        const bool rq = rot && c < p.width, rk = rot && c >= p.width && c < 2 * p.width;
-        const int pair = (c & 63) >> 1;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          const int r = 32 * j + col;
-          float4 v = make_float4(acc[j][4 * q] + bias[q].x, acc[j][4 * q + 1] + bias[q].y,
-                                 acc[j][4 * q + 2] + bias[q].z, acc[j][4 * q + 3] + bias[q].w);
-          if (rq || rk) {
-            // (cos, sin) of pairs `pair` and `pair` + 1 (one 16-byte chunk).
-            const float4 t = *reinterpret_cast<const float4*>(
-                cs + r * 64 + (((pair >> 1) ^ (r & 15)) << 2));
-            // Pair (c, c+1): y_c = x_c cos - x_{c+1} sin, y_{c+1} = x_{c+1} cos + x_c sin.
-            float4 y = make_float4(v.x * t.x - v.y * t.y, v.y * t.x + v.x * t.y,
-                                   v.z * t.z - v.w * t.w, v.w * t.z + v.z * t.w);
-            if (rq) {
-              const float s = 0.125f * p.q_scale;
-              y = make_float4(y.x * s, y.y * s, y.z * s, y.w * s);
-            }
-            v = y;
-          }
-          packed[q][j] = u32x2{pack_h2(v.x, v.y), pack_h2(v.z, v.w)};
-        }
-      }
-#pragma unroll
-      for (int qq = 0; qq < 4; qq += 2)
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-          // Low lanes: own columns 8(qq+1) .. +3 and the partner's 8(qq+1) + 4 .. +7; high lanes:
-          // the partner's 8 qq .. +3 and own 8 qq + 4 .. +7.
-          u32x4 w;
-#pragma unroll
-          for (int d = 0; d < 2; d++) {
-            const auto sw = __builtin_amdgcn_permlane32_swap(packed[qq + 1][j][d],
-                                                             packed[qq][j][d], false, false);
-            const unsigned lo = sw[0], hi = sw[1];
-            w[d] = lo;
-            w[2 + d] = hi;
-          }
-          const int r = 32 * j + col;
-          __builtin_amdgcn_raw_buffer_store_b128(
-              w, outr, ((unsigned)r * p.cols + 8 * (1 - half)) * 2, (unsigned)(32 * b + 8 * qq) * 2,
-              0);
-        }
-    }
-    __syncthreads();  // the next row block rewrites LDS
-  }
-}
-
-template <int SD>
-hipError_t launch_direct(const QkvParams& p, hipStream_t stream) {
-  const int cus = device_cus();
-  const int blocks = (p.rows + 127) / 128;
-  const int grid = blocks < cus ? blocks : cus;
-  hipLaunchKernelGGL((qkv_direct_kernel<SD>), dim3(grid), dim3(kWaves * 64), 0, stream, p);
-  return hipGetLastError();
-}
-
 template <int SD, int NR = 4>
 hipError_t launch_t(const QkvParams& p, hipStream_t stream) {
   const int cus = device_cus();
@@ -436,7 +280,7 @@ hipError_t launch_qkv(const QkvParams& p, hipStream_t stream) {
     case 128: return launch_t<8>(p, stream);
     case 256: return launch_t<16>(p, stream);
     case 384: return launch_t<24>(p, stream);
-    default: return launch_direct<32>(p, stream);
+    default: return launch_t<32, 3>(p, stream);
   }
 }
 
