@@ -20,7 +20,8 @@
 // written non-temporally (the projection is read once, by the next kernel). Measured against
 // stores of 32-byte row pieces from the accumulators: the 320 MB output costs ~26 % of the
 // kernel that way, whole lines through the caches save 10 % of it, non-temporal whole lines 17 %.
-// An odd last block is split by row tile over the first four (three) waves. No
+// An odd last block is split by row tile over the first four (three) waves, its first weight
+// steps loaded by the ring of each wave's last pair. No
 // barriers inside the column walk, so the two waves of a SIMD drift apart and one's epilogue
 // runs beside the other's MFMAs. At dim 512 the operand rows, tables and staging areas of 96
 // rows fill 152 KB of the LDS.
@@ -130,10 +131,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
 
+    // The A fragments of block 2 pr (x = 0) and 2 pr + 1 (x = 1) stream through the ring across
+    // the wave's pairs; the last pair's last steps load the first steps of the odd block's tile
+    // where the wave has one.
+    const bool tile_odd = odd && wave < NR;
+    u32x4 a[PD][2];
     if (mine > 0) {
-      // The A fragments of block 2 pr (x = 0) and 2 pr + 1 (x = 1) stream through the ring
-      // across the wave's pairs.
-      u32x4 a[PD][2];
 #pragma unroll
       for (int i = 0; i < PD; i++)
 #pragma unroll
@@ -152,11 +155,16 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
         for (int x = 0; x < 2; x++)
 #pragma unroll
           for (int j = 0; j < NR; j++) acc[x][j] = mfma32_zero();
-        // Fragment offsets of this pair's first block and of the next pair's (the last pair
-        // reloads itself: unconditional loads keep the ring in fixed registers).
+        // Fragment offsets of this pair's first block and of what follows it (x = 0, 1): the
+        // next pair's two blocks, the odd block (both streams: the second is not used) after
+        // the last pair, or else the last pair itself again (unconditional loads keep the ring in
+        // fixed registers).
         const unsigned here = (unsigned)(2 * pr * SD * kFrag);
-        const unsigned next =
-            (unsigned)(2 * min(pr + kWaves, wave + kWaves * (mine - 1)) * SD * kFrag);
+        const bool last = n == mine - 1;
+        const unsigned next0 = !last      ? (unsigned)(2 * (pr + kWaves) * SD * kFrag)
+                               : tile_odd ? (unsigned)((blocks - 1) * SD * kFrag)
+                                          : here;
+        const unsigned next1 = last && tile_odd ? next0 : next0 + (unsigned)(SD * kFrag);
 #pragma unroll
         for (int s = 0; s < SD; s++) {
           u32x4 cur[2];
@@ -164,7 +172,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
           for (int x = 0; x < 2; x++) {
             cur[x] = a[s % PD][x];
             const unsigned off = s + PD < SD ? here + (x * SD + s + PD) * kFrag
-                                             : next + (x * SD + s + PD - SD) * kFrag;
+                                             : (x ? next1 : next0) + (s + PD - SD) * kFrag;
             a[s % PD][x] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane16, off, 0);
           }
           // Operand reads and MFMAs of one step; the scheduling barrier keeps the compiler from
@@ -207,26 +215,28 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
         }
       }
     }
-    if (odd && wave < NR) {
-      // The last block: row tile `wave` of it (one MFMA per k step).
+    if (tile_odd) {
+      // The last block: row tile `wave` of it (one MFMA per k step), its first PD steps already
+      // in the ring when the wave had pairs.
       const int b = blocks - 1, j = wave;
       f32x16 acc = mfma32_zero();
-      u32x4 a[PD];
+      if (mine == 0) {
 #pragma unroll
-      for (int i = 0; i < PD; i++)
-        a[i] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane16, (unsigned)((b * SD + i) * kFrag),
-                                                     0);
+        for (int i = 0; i < PD; i++)
+          a[i][0] = __builtin_amdgcn_raw_buffer_load_b128(wr, lane16,
+                                                          (unsigned)((b * SD + i) * kFrag), 0);
+      }
+      float4 bias[4];
+      load_bias(b, bias);
 #pragma unroll
       for (int s = 0; s < SD; s++) {
-        const u32x4 cur = a[s % PD];
+        const u32x4 cur = a[s % PD][0];
         if (s + PD < SD)
-          a[s % PD] = __builtin_amdgcn_raw_buffer_load_b128(
+          a[s % PD][0] = __builtin_amdgcn_raw_buffer_load_b128(
               wr, lane16, (unsigned)((b * SD + s + PD) * kFrag), 0);
         const u32x4 bf = *reinterpret_cast<const u32x4*>(lds + (j * SD + s) * kFrag + lane16);
         acc = mfma32(cur, bf, acc);
       }
-      float4 bias[4];
-      load_bias(b, bias);
       u32x2 packed[4];
       tile_values(acc, b, j, bias, packed);
       // Lanes l and l + 32 trade halves (v_permlane32_swap) so each holds 8 consecutive columns
