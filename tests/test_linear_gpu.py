@@ -305,16 +305,19 @@ def test_block_wide_rows(gpu):
     assert err < 2e-3
 
 
+@pytest.mark.parametrize("heads", [3, 1])
 @pytest.mark.parametrize("tokens", [60, 130])
-def test_block_odd_head_count(gpu, tokens):
-    """3 heads (inner 192): the attention kernels' one-head items (an odd head count cannot be
-    paired) on the block's packed fp16 projection, band (T <= 64) and long-sequence lengths."""
-    dim, heads, hidden, groups = 128, 3, 512, 2
+def test_block_odd_head_count(gpu, tokens, heads):
+    """3 heads (inner 192) and 1 head (inner 64): the attention kernels' one-head items (an odd
+    head count cannot be paired) on the block's packed fp16 projection, band (T <= 64) and
+    long-sequence lengths. With one head the projection has 7 column blocks: three pairs, and
+    an odd block whose row tiles go to waves 0-3, wave 3 holding no pair of its own."""
+    dim, hidden, groups = 128, 512, 2
     w = _block_weights(dim, heads, hidden, normalized=True)
     x = W.normal((groups, tokens, dim), 90 + tokens, 1.0)
     block = roformer.Transformer(w, gpu)
     got = block(dev(x, gpu), roformer.axis_rope(W.rope_freqs(), tokens, gpu)).cpu().numpy()
     want = O.transformer_forward(w, x, kernels=True)
     err = float(np.abs(got - want).max())
-    print(f"block 3 heads, T={tokens}: max|diff| {err:.3e}", flush=True)
+    print(f"block {heads} heads, T={tokens}: max|diff| {err:.3e}", flush=True)
     assert err < 2e-3
