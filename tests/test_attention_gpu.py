@@ -101,8 +101,10 @@ def oracle_slice(q, k, v, table, groups):
     return O.attention_op(pick(q), pick(k), pick(v), rope=table)
 
 
-@pytest.mark.parametrize("tokens", [2, 60, 62, 64, 65, 127, 128, 129, 801, 1101])
+@pytest.mark.parametrize("tokens", [2, 60, 62, 64, 65, 127, 128, 129, 530, 640, 641, 801, 1101])
 def test_rope_on_load_matches_oracle(gpu, tokens):
+    """T = 530, 640 and 1101 end in a partial query block of at most four 32-query tiles after
+    whole 512-query blocks, 641 in one of five."""
     groups = 3 if tokens > 200 else 5
     q, k, v = seeded((groups, tokens, 8, 64), gpu)
     table = W.axis_rope_packed(W.rope_freqs(), tokens)
@@ -111,7 +113,8 @@ def test_rope_on_load_matches_oracle(gpu, tokens):
     check(f"rope T={tokens}", got, expected)
 
 
-@pytest.mark.parametrize("tokens,table_offset", [(60, 0), (130, 0), (801, 0), (130, 1), (801, 1)])
+@pytest.mark.parametrize("tokens,table_offset", [(60, 0), (130, 0), (801, 0), (130, 1), (801, 1),
+                                                (1101, 0), (1101, 1)])
 def test_gated_rope_on_unaligned_packed_rows(gpu, tokens, table_offset):
     # RoPE on load with rows whose stride is not a multiple of 4 floats (q | k | v | gates |
     # 6 zero columns: 585 per row): the element-wise load path of both attention kernels; with
@@ -294,7 +297,7 @@ def test_tail_keys_are_attended_and_padding_is_masked(gpu, tokens):
     check(f"tail keys T={tokens}", got, expected)
 
 
-@pytest.mark.parametrize("tokens", [96, 128, 130, 801])
+@pytest.mark.parametrize("tokens", [96, 128, 130, 801, 1101])
 def test_time_attention_is_repeatable(gpu, tokens):
     """Three calls on the same inputs give identical bits, and all of them match the oracle.
     Every query block of a wave is covered (T = 96 ends inside a wave's second 32-query block).
