@@ -448,6 +448,11 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
     o[0] = zero16();
     o[1] = zero16();
     float negm = 0.f, lsum = 0.f;  // -(running maximum), this lane's share of the row sum
+    // fp16 input (109 registers otherwise): -m held in a register tuple, the C operand of every
+    // block's first score MFMA, rebuilt only when the running maximum moves; fp32 input (119)
+    // builds it per block.
+    constexpr bool kSeedReg = XH;
+    f32x16 sd = {};
     // The running maximum starts at the exact maximum over the first 32 keys (T > 64); their
     // scores are kept for the first block, which then needs no score MFMAs of its own.
     f32x16 s0 = zero16();
@@ -458,6 +463,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
 #pragma unroll
       for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, s0[r]), s0[r + 1]);
       negm = -pair_max(fmaxf(mx, s0[15]));
+      if constexpr (kSeedReg) sd = seed16(negm);
     }
 
     // One 32-key block kb of the tile in buffer b. MASK: keys at or past T may be present.
@@ -470,9 +476,15 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
       if constexpr (FIRST) {
         s = s0 + negm;
       } else {
-        s = seed16(negm);
+        if constexpr (kSeedReg) {
+          s = mfma32(lds16(K + fq[0]), qf[0], sd);
 #pragma unroll
-        for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(K + fq[ds]), qf[ds], s);
+          for (int ds = 1; ds < 4; ds++) s = mfma32(lds16(K + fq[ds]), qf[ds], s);
+        } else {
+          s = seed16(negm);
+#pragma unroll
+          for (int ds = 0; ds < 4; ds++) s = mfma32(lds16(K + fq[ds]), qf[ds], s);
+        }
       }
       if constexpr (MASK) {
 #pragma unroll
@@ -490,6 +502,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void attention_long_kernel(AttnPara
         if (cm > kTau) {
           const float alpha = fast_exp2(-cm);
           negm -= cm;
+          if constexpr (kSeedReg) sd = seed16(negm);
           s -= cm;
           o[0] *= alpha;
           o[1] *= alpha;
