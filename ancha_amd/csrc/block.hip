@@ -43,6 +43,29 @@ struct ancha_hip_block {
   _Float16* packed_frag = nullptr;
 };
 
+namespace ancha {
+
+// Fragment-major copy of W^T [rows][k] (k contiguous) for the A operand of the 32x32x16 MFMA
+// in tail.hip: fragment (b, s) is 512 halves at (b * (k / 16) + s) * 512, lane l's 8 at 8 l,
+// holding W^T[32 b + l % 32][16 s + perm(8 (l / 32) + t)] for t < 8, perm = kPerm16 (or the
+// identity). rows % 32 == 0, k % 16 == 0.
+std::vector<_Float16> fragment_major(const std::vector<_Float16>& wt, size_t rows, size_t k,
+                                     bool permute) {
+  std::vector<_Float16> out(rows * k);
+  const size_t steps = k / 16;
+  for (size_t b = 0; b < rows / 32; b++)
+    for (size_t s = 0; s < steps; s++)
+      for (size_t l = 0; l < 64; l++)
+        for (size_t t = 0; t < 8; t++) {
+          const size_t kk = 8 * (l / 32) + t;
+          const size_t src = 16 * s + (permute ? static_cast<size_t>(ancha::kPerm16[kk]) : kk);
+          out[((b * steps + s) * 64 + l) * 8 + t] = wt[(32 * b + l % 32) * k + src];
+        }
+  return out;
+}
+
+}  // namespace ancha
+
 namespace {
 
 constexpr size_t kHeadDim = ANCHA_ATTENTION_HEAD_DIM;
@@ -76,25 +99,6 @@ int upload(const std::vector<T>& host, T** dev) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
-
-// Fragment-major copy of W^T [rows][k] (k contiguous) for the A operand of the 32x32x16 MFMA
-// in tail.hip: fragment (b, s) is 512 halves at (b * (k / 16) + s) * 512, lane l's 8 at 8 l,
-// holding W^T[32 b + l % 32][16 s + perm(8 (l / 32) + t)] for t < 8, perm = kPerm16 (or the
-// identity). rows % 32 == 0, k % 16 == 0.
-std::vector<_Float16> fragment_major(const std::vector<_Float16>& wt, size_t rows, size_t k,
-                                     bool permute) {
-  std::vector<_Float16> out(rows * k);
-  const size_t steps = k / 16;
-  for (size_t b = 0; b < rows / 32; b++)
-    for (size_t s = 0; s < steps; s++)
-      for (size_t l = 0; l < 64; l++)
-        for (size_t t = 0; t < 8; t++) {
-          const size_t kk = 8 * (l / 32) + t;
-          const size_t src = 16 * s + (permute ? static_cast<size_t>(ancha::kPerm16[kk]) : kk);
-          out[((b * steps + s) * 64 + l) * 8 + t] = wt[(32 * b + l % 32) * k + src];
-        }
-  return out;
-}
 
 // One block GEMM through the fp16-weight kernel.
 int gemm(const void* x, bool x_half, size_t n, size_t k, const _Float16* wt, size_t m,
@@ -373,12 +377,12 @@ int ancha_hip_block_create(size_t dim, size_t heads, size_t hidden, const float*
   if (!rc) rc = upload(os, &b->out_scale);
   if (!rc && ancha::block_tail_supported(static_cast<int>(dim), static_cast<int>(inner),
                                          static_cast<int>(hidden))) {
-    rc = upload(fragment_major(ow, dim, inner, false), &b->wo_frag);
-    if (!rc) rc = upload(fragment_major(w1, hidden, dim, true), &b->w1_frag);
-    if (!rc) rc = upload(fragment_major(w2, dim, hidden, true), &b->w2_frag);
+    rc = upload(ancha::fragment_major(ow, dim, inner, false), &b->wo_frag);
+    if (!rc) rc = upload(ancha::fragment_major(w1, hidden, dim, true), &b->w1_frag);
+    if (!rc) rc = upload(ancha::fragment_major(w2, dim, hidden, true), &b->w2_frag);
   }
   if (!rc && ancha::qkv_supported(static_cast<int>(dim), static_cast<int>(columns)))
-    rc = upload(fragment_major(pw, columns, dim, false), &b->packed_frag);
+    rc = upload(ancha::fragment_major(pw, columns, dim, false), &b->packed_frag);
   if (rc) {
     ancha_hip_block_destroy(b);
     return rc;

@@ -3,6 +3,8 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <vector>
+
 #include "../../include/ancha_hip.h"
 
 namespace ancha {
@@ -158,9 +160,22 @@ struct QkvParams {
   int rows, dim, cols;
   int tokens, token_div, width;
   float q_scale;
+  // launch_mask_hidden only: `batch` products, product b reading xh + b * x_bstride, w +
+  // b * w_bstride, bias + b * b_bstride and writing out + b * out_bstride (elements).
+  int batch;
+  long x_bstride, w_bstride, b_bstride, out_bstride;
 };
 bool qkv_supported(int dim, int cols);
 hipError_t launch_qkv(const QkvParams& p, hipStream_t stream);
+// The mask heads' first hidden layer on the same kernel: out = fp16(tanh(xh . W^T + bias)) for
+// every column (cols % 64 == 0), per band product, W^T fragment-major as in the block.
+bool mask_hidden_supported(int dim, int cols);
+// Fragment-major copy of W^T [rows][k] (host side, at weight load): fragment (b, s) = 512
+// halves at (b * (k / 16) + s) * 512, lane l's 8 at 8 l, holding W^T[32 b + l % 32][16 s +
+// perm(8 (l / 32) + t)], perm = kPerm16 (permute) or the identity. rows % 32 == 0, k % 16 == 0.
+std::vector<_Float16> fragment_major(const std::vector<_Float16>& wt, size_t rows, size_t k,
+                                     bool permute);
+hipError_t launch_mask_hidden(const QkvParams& p, hipStream_t stream);
 
 // Order of k within each 16-block of a fragment-major weight whose B operand comes straight
 // from another product's accumulators (tail.hip): B k-slot 8h + t holds feature kPerm16[8h + t].

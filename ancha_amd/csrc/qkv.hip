@@ -20,6 +20,8 @@
 // written non-temporally (the projection is read once, by the next kernel). Measured against
 // stores of 32-byte row pieces from the accumulators: the 320 MB output costs ~26 % of the
 // kernel that way, whole lines through the caches save 10 % of it, non-temporal whole lines 17 %.
+// The same kernel (TANH) runs the mask heads' first hidden layer: bias + tanh on every column,
+// per-band products of `rows` rows, a band's row blocks on one XCD.
 // An odd last block is split by row tile over the first four (three) waves, its first weight
 // steps loaded by the ring of each wave's last pair. No
 // barriers inside the column walk, so the two waves of a SIMD drift apart and one's epilogue
@@ -27,6 +29,7 @@
 // rows fill 152 KB of the LDS.
 #include "buffer.hpp"
 #include "common.hpp"
+#include "gemm.hpp"
 #include "kernels.hpp"
 
 namespace ancha {
@@ -36,7 +39,9 @@ constexpr int kWaves = 8;
 constexpr int kFrag = 1024;
 
 // SD = dim / 16 k steps (dims 128 - 512); NR 32-row tiles per row block (4; 3 at dim 512).
-template <int SD, int NR>
+// TANH: the mask heads' hidden layer (bias + tanh on every column, no rotary table, p.batch
+// products of p.rows rows each).
+template <int SD, int NR, bool TANH = false>
 __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
   constexpr int kRows = 32 * NR;
   constexpr int kX = kRows * SD * 16 * 2;      // operand fragments
@@ -58,13 +63,14 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
   const int half = lane >> 5, col = lane & 31;
   const unsigned lane16 = (unsigned)lane * 16;
   const int dim = SD * 16;
-  const int used = 3 * p.width + p.width / 64;   // q, k, v and one gate column per head
+  // q, k, v and one gate column per head (all columns for TANH)
+  const int used = TANH ? p.cols : 3 * p.width + p.width / 64;
   const int blocks = (used + 31) / 32;
   const int pairs = blocks / 2;
   const bool odd = (blocks & 1) != 0;
-  const rsrc_t wr = make_rsrc(p.w, (unsigned)(p.cols * dim * 2));
-  const rsrc_t br = make_rsrc(p.bias, (unsigned)(p.cols * 4));
-  const rsrc_t tr = make_rsrc(p.rope, (unsigned)(4 * p.tokens * 256));
+  rsrc_t wr = make_rsrc(p.w, (unsigned)(p.cols * dim * 2));
+  rsrc_t br = make_rsrc(p.bias, (unsigned)(p.cols * 4));
+  const rsrc_t tr = make_rsrc(TANH ? p.bias : p.rope, TANH ? 0u : (unsigned)(4 * p.tokens * 256));
 
   auto load_bias = [&](int b, float4 (&bias)[4]) {
 #pragma unroll
@@ -84,7 +90,10 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
       const int pair = ((32 * b + 8 * q + 4 * half) & 63) >> 1;
       float4 v = make_float4(acc[4 * q] + bias[q].x, acc[4 * q + 1] + bias[q].y,
                              acc[4 * q + 2] + bias[q].z, acc[4 * q + 3] + bias[q].w);
-      if (rq || rk) {
+      if constexpr (TANH) {
+        v = make_float4(gemm::tanh_fast(v.x), gemm::tanh_fast(v.y), gemm::tanh_fast(v.z),
+                        gemm::tanh_fast(v.w));
+      } else if (rq || rk) {
         // (cos, sin) of pairs `pair` and `pair` + 1 (one 16-byte chunk).
         const float4 t = *reinterpret_cast<const float4*>(
             cs + r * 64 + (((pair >> 1) ^ (r & 15)) << 2));
@@ -108,11 +117,24 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
   constexpr int PD = SD % 4 == 0 && SD > 16 ? 4 : 2;
   static_assert(SD % PD == 0 && SD >= PD, "K steps come in groups of PD");
 
-  for (int blk = blockIdx.x; blk * kRows < p.rows; blk += gridDim.x) {
-    const int row0 = blk * kRows;
+  // Row blocks of each product (one product unless TANH).
+  const int bpi = (p.rows + kRows - 1) / kRows;
+  const int total = TANH ? bpi * p.batch : bpi;
+  // TANH: each product has weights of its own, so the row blocks of one product are kept on one
+  // XCD (consecutive logical ids share an XCD) and its weights come into that XCD's L2 once.
+  const int first = TANH ? xcd_remap(blockIdx.x, gridDim.x) : (int)blockIdx.x;
+  for (int blk = first; blk < total; blk += gridDim.x) {
+    const int item = TANH ? blk / bpi : 0;
+    const int row0 = (blk - item * bpi) * kRows;
     const int nrows = min(kRows, p.rows - row0);
-    const rsrc_t xr = make_rsrc(p.xh + (long)row0 * dim, (unsigned)(nrows * dim * 2));
-    const rsrc_t outr = make_rsrc(p.out + (long)row0 * p.cols, (unsigned)(nrows * p.cols * 2));
+    const rsrc_t xr = make_rsrc(p.xh + item * p.x_bstride + (long)row0 * dim,
+                                (unsigned)(nrows * dim * 2));
+    const rsrc_t outr = make_rsrc(p.out + item * p.out_bstride + (long)row0 * p.cols,
+                                  (unsigned)(nrows * p.cols * 2));
+    if constexpr (TANH) {
+      wr = make_rsrc(p.w + item * p.w_bstride, (unsigned)(p.cols * dim * 2));
+      br = make_rsrc(p.bias + item * p.b_bstride, (unsigned)(p.cols * 4));
+    }
     // Operand rows as B fragments: fragment (jb, s) = rows 32 jb + (l % 32), k 16 s + 8 (l / 32).
     for (int f = wave; f < NR * SD; f += kWaves) {
       const int jb = f / SD, s = f % SD;
@@ -121,7 +143,7 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
           ((unsigned)(32 * jb + col) * dim + 16 * s + 8 * half) * 2, 0, 0, 0);
     }
     // Key-table cos / sin of each row's token (the query tables are these times 1/8).
-    for (int e = tid; e < kRows * 32; e += kWaves * 64) {
+    for (int e = tid; e < (TANH ? 0 : kRows * 32); e += kWaves * 64) {
       const int r = e >> 5, i = e & 31;
       const int tok = ((row0 + r) / p.token_div) % p.tokens;
       float* slot = cs + r * 64 + (((i >> 1) ^ (r & 15)) << 2) + 2 * (i & 1);
@@ -264,12 +286,12 @@ __global__ __launch_bounds__(kWaves * 64, 1) void qkv_kernel(QkvParams p) {
   }
 }
 
-template <int SD, int NR = 4>
+template <int SD, int NR = 4, bool TANH = false>
 hipError_t launch_t(const QkvParams& p, hipStream_t stream) {
   const int cus = device_cus();
-  const int blocks = (p.rows + 32 * NR - 1) / (32 * NR);
+  const int blocks = (p.rows + 32 * NR - 1) / (32 * NR) * (TANH ? p.batch : 1);
   const int grid = blocks < cus ? blocks : cus;
-  hipLaunchKernelGGL((qkv_kernel<SD, NR>), dim3(grid), dim3(kWaves * 64), 0, stream, p);
+  hipLaunchKernelGGL((qkv_kernel<SD, NR, TANH>), dim3(grid), dim3(kWaves * 64), 0, stream, p);
   return hipGetLastError();
 }
 
@@ -292,6 +314,17 @@ hipError_t launch_qkv(const QkvParams& p, hipStream_t stream) {
     case 384: return launch_t<24>(p, stream);
     default: return launch_t<32, 3>(p, stream);
   }
+}
+
+bool mask_hidden_supported(int dim, int cols) {
+  return (dim == 384 || dim == 512) && cols > 0 && cols % 64 == 0;
+}
+
+hipError_t launch_mask_hidden(const QkvParams& p, hipStream_t stream) {
+  if (!mask_hidden_supported(p.dim, p.cols) || p.batch <= 0 || !p.bias)
+    return hipErrorInvalidValue;
+  if (p.rows <= 0) return hipSuccess;
+  return p.dim == 384 ? launch_t<24, 4, true>(p, stream) : launch_t<32, 3, true>(p, stream);
 }
 
 }  // namespace ancha

@@ -66,6 +66,7 @@ struct ancha_hip_roformer {
   struct Head {
     std::vector<_Float16*> hw;
     std::vector<float*> hb;
+    bool frag0 = false;  // hw[0] fragment-major per band (launch_mask_hidden)
     _Float16* ow = nullptr;
     float* ob = nullptr;
   };
@@ -275,10 +276,28 @@ int forward_impl(ancha_hip_roformer* m, const float* const* spectra, size_t nch,
     size_t in_dim = m->dim;
     for (size_t layer = 0; layer < m->mask_layers; layer++) {
       _Float16* out = h[layer & 1];
-      const int rc = gemm(in, in_half, frames, in_dim, head.hw[layer], mh, head.hb[layer], true,
-                          out, true, m->bands, static_cast<long>(frames * in_dim),
-                          static_cast<long>(mh * in_dim), static_cast<long>(mh),
-                          static_cast<long>(frames * mh), stream);
+      int rc = 0;
+      if (layer == 0 && head.frag0 && in_half) {
+        ancha::QkvParams qp{};
+        qp.xh = static_cast<const _Float16*>(in);
+        qp.w = head.hw[0];
+        qp.bias = head.hb[0];
+        qp.out = out;
+        qp.rows = static_cast<int>(frames);
+        qp.dim = static_cast<int>(in_dim);
+        qp.cols = static_cast<int>(mh);
+        qp.batch = static_cast<int>(m->bands);
+        qp.x_bstride = static_cast<long>(frames * in_dim);
+        qp.w_bstride = static_cast<long>(mh * in_dim);
+        qp.b_bstride = static_cast<long>(mh);
+        qp.out_bstride = static_cast<long>(frames * mh);
+        rc = ancha::hip_status(ancha::launch_mask_hidden(qp, stream), kWhere);
+      } else {
+        rc = gemm(in, in_half, frames, in_dim, head.hw[layer], mh, head.hb[layer], true, out,
+                  true, m->bands, static_cast<long>(frames * in_dim),
+                  static_cast<long>(mh * in_dim), static_cast<long>(mh),
+                  static_cast<long>(frames * mh), stream);
+      }
       if (rc) return rc;
       in = out;
       in_half = true;
@@ -550,6 +569,18 @@ int ancha_hip_roformer_create(const ancha_hip_roformer_config* c, ancha_hip_tens
       }
       _Float16* dw = nullptr;
       float* db = nullptr;
+      // The first hidden layer (fp16 input, dim 384 / 512) runs on the projection kernel, which
+      // takes W^T fragment-major per band.
+      if (layer == 0 && ancha::mask_hidden_supported(static_cast<int>(in), static_cast<int>(mh))) {
+        std::vector<_Float16> f(w.size());
+        for (size_t b = 0; b < c->bands; b++) {
+          const std::vector<_Float16> one(w.begin() + b * mh * in, w.begin() + (b + 1) * mh * in);
+          const std::vector<_Float16> fm = ancha::fragment_major(one, mh, in, false);
+          std::copy(fm.begin(), fm.end(), f.begin() + b * mh * in);
+        }
+        w.swap(f);
+        h.frag0 = true;
+      }
       rc = upload(w, &dw);
       h.hw.push_back(dw);
       if (!rc) rc = upload(bias, &db);
